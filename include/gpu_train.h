@@ -1,0 +1,96 @@
+/* gpu_train.h -- GPU-resident training of the turkce-llm model on MI355X.
+ *
+ * Drop-in for the reference's model/gpu_train.h: every prototype below is
+ * byte-identical to model/gpu_train.h:86-125 and the two macros keep their
+ * values (gpu_train.h:30-31).  Only the private members of GpuTrainer
+ * changed: they hold HIP handles instead of CUDA ones (no caller reads
+ * them), and the activation set follows the flash-attention design (no
+ * [B,H,T,T] probability tensor; a per-row log-sum-exp instead).
+ *
+ * Semantics kept from the reference:
+ *   - flat params/grads/adam_m/adam_v buffers in lm_collect_params order;
+ *   - B sequences of T tokens stacked as N = B*T rows;
+ *   - loss = per-sequence mean, then mean over sequences (gpu_train.c:478-487);
+ *   - eval_loss == forward_backward's loss, bit for bit;
+ *   - every reduction in fixed order (no atomics): reruns are bit-identical;
+ *   - errors print a diagnostic and end the process (_exit(1)).
+ */
+#ifndef MODEL_GPU_TRAIN_H
+#define MODEL_GPU_TRAIN_H
+
+#include "trlm_host.h"
+#include "hip_backend.h"
+
+#define GPU_TRAIN_MAX_PARAMS (LM_MAX_LAYERS * 10u + 2u)
+#define GPU_TRAIN_NORM_BLOCKS 1024u
+
+typedef struct GpuLayerActs {
+    hipDeviceptr_t x_in;   /* [N,D] layer input (residual stream) */
+    hipDeviceptr_t n1;     /* [N,D] attention RMSNorm output */
+    hipDeviceptr_t r1;     /* [N]   1/rms */
+    hipDeviceptr_t qkv;    /* [N,3D] projection, RoPE applied to Q and K */
+    hipDeviceptr_t att;    /* [N,D] attention output, heads side by side */
+    hipDeviceptr_t lse;    /* [B*H*T] base-2 log-sum-exp of the scaled scores */
+    hipDeviceptr_t x2;     /* [N,D] */
+    hipDeviceptr_t n2;     /* [N,D] */
+    hipDeviceptr_t r2;     /* [N] */
+    hipDeviceptr_t gu;     /* [N,2F] gate | up */
+    hipDeviceptr_t h;      /* [N,F] */
+} GpuLayerActs;
+
+typedef struct TrlmGemm TrlmGemm;
+
+typedef struct GpuKernels {
+    hipFunction_t fill_zero, embed_fwd, embed_bwd, rmsnorm_fwd, rmsnorm_bwd, colsum_partial, colsum_final;
+    hipFunction_t rope_qk, swiglu_fwd, swiglu_bwd, cross_entropy, argmax_rows, sumsq_partial, adam;
+    hipFunction_t attn_fwd, attn_bwd_prep, attn_bwd_dkv, attn_bwd_dq;
+} GpuKernels;
+
+typedef struct GpuTrainer {
+    HipCtx hip;
+    GpuKernels k;
+    TrlmGemm* gemm;
+
+    u32 V, D, H, L, F, T, B, N, hd;
+    f32 eps;
+    u32 ldv;            /* logits row stride: V rounded up to a multiple of 4 */
+
+    u32 num_params;
+    u64 offsets[GPU_TRAIN_MAX_PARAMS];
+    u64 numels[GPU_TRAIN_MAX_PARAMS];
+    u64 total_scalars;
+    hipDeviceptr_t params, grads, adam_m, adam_v;
+
+    GpuLayerActs layers[LM_MAX_LAYERS];
+    hipDeviceptr_t x_final, nf, rf, logits;   /* logits [N, ldv]: gradient after the CE */
+
+    hipDeviceptr_t dres, dn, datt, dqkv, dh, dgu, dvec, part;
+
+    hipDeviceptr_t ids, targets, loss_rows, cos_t, sin_t;
+    hipDeviceptr_t emb_order, emb_seg;        /* embedding-backward row groups */
+    u32 emb_nseg;
+    f32* host_loss_rows;                      /* [N] */
+    u32* host_emb;                            /* [N + 2N + 1 + V + 1] */
+    hipDeviceptr_t norm_partial;              /* [GPU_TRAIN_NORM_BLOCKS] */
+    f32* host_norm_partial;
+} GpuTrainer;
+
+GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,
+                              Node** params, u32 num_params, u32 batch_size, u32 seq_len);
+void gpu_trainer_destroy(GpuTrainer* g);
+
+void gpu_trainer_upload(GpuTrainer* g, Node** params, const AdamOptimizer* opt);
+void gpu_trainer_download(GpuTrainer* g, Node** params, AdamOptimizer* opt);
+void gpu_trainer_download_grads(GpuTrainer* g, Node** params);
+void gpu_trainer_upload_grads(GpuTrainer* g, Node** params);
+
+void gpu_trainer_sample_batch(const u32* tokens, u64 num_tokens, u32 seq_len, u32 batch_size,
+                              u64 seed_base, u32* ids_out, u32* targets_out);
+
+f32 gpu_trainer_forward_backward(GpuTrainer* g, const u32* ids, const u32* targets);
+f32 gpu_trainer_eval_loss(GpuTrainer* g, const u32* ids, const u32* targets);
+f64 gpu_trainer_grad_norm(GpuTrainer* g);
+void gpu_trainer_adam_step(GpuTrainer* g, AdamOptimizer* opt);
+void gpu_trainer_adam_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 grad_scale);
+
+#endif /* MODEL_GPU_TRAIN_H */

@@ -1,0 +1,71 @@
+/* hip_backend.h -- thin HIP module-API backend for gfx950 code objects.
+ *
+ * Takes the role of the reference's CUDA Driver-API backend
+ * (cuda/cuda_backend.h:9-65, cuda/driver_api.h): a context loads one kernel
+ * image, kernels are looked up by name and launched with a `void**` argument
+ * array, memory is allocated/copied synchronously, and any failure prints a
+ * diagnostic and ends the process with _exit(1) (cuda_backend.c:15-34).
+ *
+ * MI355X-specific choices:
+ *   - the image is a gfx950 code object (.hsaco from hipcc --genco), loaded
+ *     with hipModuleLoadData: no JIT step, unlike the reference's PTX;
+ *   - every context owns one HIP stream at default priority; launches and
+ *     copies go to the stream of the context made current on the calling
+ *     thread (hip_set_current), and the blocking helpers synchronise it, so
+ *     callers see the reference's in-order, synchronous behaviour;
+ *   - HIP has no context destroy that frees memory, so a context records
+ *     the buffers allocated while it is current and hip_shutdown frees them.
+ */
+#ifndef HIP_BACKEND_H
+#define HIP_BACKEND_H
+
+#ifndef __HIP_PLATFORM_AMD__
+#define __HIP_PLATFORM_AMD__
+#endif
+#include <hip/hip_runtime_api.h>
+
+#include "trlm_host.h"
+
+typedef struct HipAllocList HipAllocList;
+
+typedef struct HipCtx {
+    i32 device;
+    hipModule_t module;
+    hipStream_t stream;
+    HipAllocList* allocs;
+} HipCtx;
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* cuda_init / cuda_init_on_device (cuda_backend.h:19,29). image_path names a
+ * gfx950 code object; it is read into `scratch`. */
+HipCtx hip_init(Allocator* scratch, const char* image_path);
+HipCtx hip_init_on_device(Allocator* scratch, const char* image_path, i32 device_index);
+i32 hip_device_count(void);                                   /* cuda_backend.h:32 */
+void hip_shutdown(HipCtx* c);                                 /* cuda_backend.h:34 */
+void hip_set_current(HipCtx* c);                              /* cuda_backend.h:40 */
+hipFunction_t hip_get_kernel(HipCtx* c, const char* name);    /* cuda_backend.h:42 */
+
+hipDeviceptr_t hip_alloc(u64 bytes);                          /* cuda_backend.h:44-47 */
+void hip_free(hipDeviceptr_t p);
+void hip_h2d(hipDeviceptr_t dst, const void* src, u64 bytes);
+void hip_d2h(void* dst, hipDeviceptr_t src, u64 bytes);
+
+void hip_launch_1d(hipFunction_t f, u32 n, void** params);    /* cuda_backend.h:50-60 */
+void hip_launch_2d(hipFunction_t f, u32 rows, u32 cols, void** params);
+void hip_launch_1d_shared(hipFunction_t f, u32 n, u32 block_size, u32 shared_bytes, void** params);
+void hip_launch(hipFunction_t f, u32 gx, u32 gy, u32 gz, u32 bx, u32 by, u32 bz, u32 shared_bytes,
+                void** params);
+void hip_memset_zero(hipDeviceptr_t p, u64 bytes);            /* cuda_backend.h:63 */
+void hip_sync(void);                                          /* cuda_backend.h:65 */
+
+/* The stream of the context current on this thread (for event timing). */
+hipStream_t hip_current_stream(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* HIP_BACKEND_H */

@@ -1,0 +1,72 @@
+/* trlm_ext.h -- additive entry points of the MI355X GPU path.
+ *
+ * None of these exist in the reference's API (model/gpu_train.h,
+ * model/gpu_ops.h); they cover what BASELINE's configurations ask for and
+ * the reference does not offer:
+ *   - forward to logits, with or without the mean cross-entropy, and greedy
+ *     argmax (the reference's CE overwrites logits with their gradient,
+ *     train_kernels.cu:742-772, and it has no GPU argmax);
+ *   - AdamW (decoupled weight decay; the reference's Adam has none,
+ *     training/adam.c:43-52);
+ *   - a raw fp32 GEMM on device buffers and stream-event timing, for the
+ *     model-shape GEMM sweep and its tests.
+ */
+#ifndef TRLM_EXT_H
+#define TRLM_EXT_H
+
+#include "gpu_train.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Forward pass only; copies logits [B*T, V] (row-major, unpadded) to
+ * host_logits when it is not NULL.  Leaves the logits on the device for
+ * gpu_trainer_greedy_argmax. */
+void gpu_trainer_forward_logits(GpuTrainer* g, const u32* ids, f32* host_logits);
+
+/* Forward pass plus mean cross-entropy (same definition and bits as
+ * gpu_trainer_eval_loss) without overwriting the logits; copies them to
+ * host_logits when not NULL. */
+f32 gpu_trainer_forward_loss_logits(GpuTrainer* g, const u32* ids, const u32* targets, f32* host_logits);
+
+/* Greedy next token of every row of the logits left on the device by the
+ * last forward: first index of the row maximum (ties -> lowest index). */
+void gpu_trainer_greedy_argmax(GpuTrainer* g, u32* host_ids_out);
+
+/* AdamW: t++, then p -= lr*m_hat/(sqrt(v_hat)+eps) + lr*weight_decay*p on
+ * all parameters (the reference has no exclusion list).  weight_decay = 0
+ * gives exactly gpu_trainer_adam_step_scaled. */
+void gpu_trainer_adamw_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay, f32 grad_scale);
+
+/* ---- raw GEMM on device buffers (current context of the calling thread) ----
+ * C = alpha*op(A)@op(B) (+ beta*C) (+ bias[n]) (+ resid[m,n]), batched with
+ * element strides; trans_a/trans_b as k_gemm_nn/nt/tn of the reference
+ * (train_kernels.cu:97-105).  bias/resid may be NULL. */
+typedef struct TrlmGemm TrlmGemm;
+TrlmGemm* trlm_gemm_create(HipCtx* ctx);
+void trlm_gemm_destroy(TrlmGemm* e);
+void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+               i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+               f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr);
+/* Name of the kernel variant and split-K factor the last trlm_gemm call used. */
+const char* trlm_gemm_last_variant(TrlmGemm* e, i32* splits);
+
+/* Stream-event timing on the current context's stream. */
+typedef struct TrlmTimer { hipEvent_t start, stop; } TrlmTimer;
+void trlm_timer_create(TrlmTimer* t);
+void trlm_timer_destroy(TrlmTimer* t);
+void trlm_timer_start(TrlmTimer* t);
+f32 trlm_timer_stop_ms(TrlmTimer* t);   /* waits for the stop event */
+
+/* Library version string (build identification) and the sizes of the
+ * by-value structures, for bindings that must allocate them. */
+const char* trlm_version(void);
+u64 trlm_sizeof_gpu_trainer(void);
+u64 trlm_sizeof_hip_ctx(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TRLM_EXT_H */

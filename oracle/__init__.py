@@ -1,0 +1,264 @@
+"""ctypes front end of the CPU oracle -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this module.  It loads oracle/liboracle.so (the C restatement of the
+reference's fp32 CPU path, trlm_oracle.c) and, when it was built,
+oracle/_ref/libtrlm_refh.so (a harness over the reference's own CPU sources,
+ref_harness.c).
+"""
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "liboracle.so")
+REF_LIB = os.path.join(HERE, "_ref", "libtrlm_ref.so")
+REF_HARNESS = os.path.join(HERE, "_ref", "libtrlm_refh.so")
+
+f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+u32p = np.ctypeslib.ndpointer(np.uint32, flags="C_CONTIGUOUS")
+u64p = np.ctypeslib.ndpointer(np.uint64, flags="C_CONTIGUOUS")
+i64p = np.ctypeslib.ndpointer(np.int64, flags="C_CONTIGUOUS")
+f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+
+
+class Cfg(C.Structure):
+    """Model dimensions (V, D, H, L, F, eps) -- layout of OrCfg / RefCfg."""
+    _fields_ = [("V", C.c_uint32), ("D", C.c_uint32), ("H", C.c_uint32),
+                ("L", C.c_uint32), ("F", C.c_uint32), ("eps", C.c_float)]
+
+
+class Pcg(C.Structure):
+    _fields_ = [("state", C.c_uint64), ("inc", C.c_uint64),
+                ("has_cached", C.c_uint32), ("cached", C.c_double)]
+
+
+def build(ref_root="/root/reference", with_ref=True):
+    """Compile liboracle.so, and oracle/_ref when the reference tree exists."""
+    subprocess.run(["make", "-s", "-C", HERE, "liboracle.so"], check=True)
+    if with_ref and os.path.isdir(ref_root):
+        subprocess.run(["make", "-s", "-C", HERE, "ref", "REF=" + ref_root], check=True)
+
+
+def _load():
+    if not os.path.exists(LIB):
+        build(with_ref=False)
+    lib = C.CDLL(LIB)
+    cfgp = C.POINTER(Cfg)
+    sig = {
+        "or_m_sqrt": (C.c_double, [C.c_double]), "or_m_exp": (C.c_double, [C.c_double]),
+        "or_m_log": (C.c_double, [C.c_double]), "or_m_pow": (C.c_double, [C.c_double, C.c_double]),
+        "or_m_sin": (C.c_double, [C.c_double]), "or_m_cos": (C.c_double, [C.c_double]),
+        "or_m_sqrtf": (C.c_float, [C.c_float]), "or_m_expf": (C.c_float, [C.c_float]),
+        "or_m_logf": (C.c_float, [C.c_float]), "or_m_powf": (C.c_float, [C.c_float, C.c_float]),
+        "or_m_sinf": (C.c_float, [C.c_float]), "or_m_cosf": (C.c_float, [C.c_float]),
+        "or_pcg_seed": (None, [C.POINTER(Pcg), C.c_uint64, C.c_uint64]),
+        "or_pcg_next_u32": (C.c_uint32, [C.POINTER(Pcg)]),
+        "or_pcg_range_i64": (C.c_int64, [C.POINTER(Pcg), C.c_int64, C.c_int64]),
+        "or_pcg_gaussian": (C.c_double, [C.POINTER(Pcg), C.c_double, C.c_double]),
+        "or_num_params": (C.c_uint32, [cfgp]),
+        "or_param_layout": (C.c_uint64, [cfgp, u64p, u64p]),
+        "or_lm_init": (None, [cfgp, C.c_uint64, C.c_uint64, f32p]),
+        "or_rope_tables": (None, [C.c_uint32, C.c_uint32, f32p, f32p]),
+        "or_sample_batch": (None, [u32p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64, u32p, u32p]),
+        "or_matmul": (None, [C.c_uint32, C.c_uint32, C.c_uint32, f32p, C.c_int64, C.c_int64,
+                             f32p, C.c_int64, C.c_int64, f32p]),
+        "or_forward_logits": (None, [cfgp, f32p, u32p, C.c_uint32, C.c_uint32, f32p, C.c_int]),
+        "or_forward_backward": (C.c_float, [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32,
+                                            C.c_void_p, C.c_void_p, C.c_int]),
+        "or_adam_step": (None, [f32p, f32p, f32p, f32p, C.c_uint64, C.c_uint64, C.c_float,
+                                C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]),
+        "or_argmax": (C.c_uint32, [f32p, C.c_uint32]),
+    }
+    for name, (res, args) in sig.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    return lib
+
+
+_lib = None
+
+
+def lib():
+    global _lib
+    if _lib is None:
+        _lib = _load()
+    return _lib
+
+
+def _threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+class Model:
+    """A model configuration plus the oracle's flat parameter layout."""
+
+    def __init__(self, V, D, H, L, F, eps=1e-5):
+        self.cfg = Cfg(V, D, H, L, F, eps)
+        self.V, self.D, self.H, self.L, self.F, self.eps = V, D, H, L, F, eps
+        n = lib().or_num_params(C.byref(self.cfg))
+        self.offsets = np.zeros(n, np.uint64)
+        self.numels = np.zeros(n, np.uint64)
+        self.total = int(lib().or_param_layout(C.byref(self.cfg), self.offsets, self.numels))
+        self.num_params = n
+
+    def shapes(self):
+        """Per-tensor shapes in lm_collect_params order (lm_model.c:134-148)."""
+        D, F = self.D, self.F
+        out = [(self.V, D)]
+        for _ in range(self.L):
+            out += [(D,), (D, 3 * D), (3 * D,), (D, D), (D,), (D,), (D, 2 * F), (2 * F,), (F, D), (D,)]
+        out.append((D,))
+        return out
+
+    def split(self, flat):
+        return [flat[int(o):int(o) + int(n)].reshape(s)
+                for o, n, s in zip(self.offsets, self.numels, self.shapes())]
+
+    def init(self, seed_a=1337, seed_b=1):
+        p = np.zeros(self.total, np.float32)
+        lib().or_lm_init(C.byref(self.cfg), seed_a, seed_b, p)
+        return p
+
+    def forward_logits(self, params, ids, B, T, nthreads=None):
+        out = np.zeros((B * T, self.V), np.float32)
+        lib().or_forward_logits(C.byref(self.cfg), params, np.ascontiguousarray(ids, np.uint32),
+                                B, T, out, nthreads or _threads())
+        return out
+
+    def forward_backward(self, params, ids, tgt, B, T, want_grads=True, nthreads=None):
+        grads = np.zeros(self.total, np.float32) if want_grads else None
+        rows = np.zeros(B * T, np.float32)
+        loss = lib().or_forward_backward(
+            C.byref(self.cfg), params, np.ascontiguousarray(ids, np.uint32),
+            np.ascontiguousarray(tgt, np.uint32), B, T,
+            grads.ctypes.data if grads is not None else None, rows.ctypes.data, nthreads or _threads())
+        return np.float32(loss), grads, rows
+
+
+def matmul(A, B):
+    """Reference-order fp32 C = A @ B (tensor.c:351-373)."""
+    A = np.ascontiguousarray(A, np.float32)
+    B = np.ascontiguousarray(B, np.float32)
+    M, K = A.shape
+    N = B.shape[1]
+    out = np.zeros((M, N), np.float32)
+    lib().or_matmul(M, N, K, A, K, 1, B, N, 1, out)
+    return out
+
+
+def rope_tables(T, hd):
+    c = np.zeros((T, hd // 2), np.float32)
+    s = np.zeros((T, hd // 2), np.float32)
+    lib().or_rope_tables(T, hd, c, s)
+    return c, s
+
+
+def sample_batch(tokens, T, B, seed_base):
+    tokens = np.ascontiguousarray(tokens, np.uint32)
+    ids = np.zeros(B * T, np.uint32)
+    tgt = np.zeros(B * T, np.uint32)
+    lib().or_sample_batch(tokens, len(tokens), T, B, seed_base, ids, tgt)
+    return ids, tgt
+
+
+def pcg_stream(seed_a, seed_b):
+    r = Pcg()
+    lib().or_pcg_seed(C.byref(r), seed_a, seed_b)
+    return r
+
+
+def random_tokens(n, V, seed_a=4242, seed_b=7, hi_exclusive=None):
+    """n token ids from pcg_range_i64(0, hi) (test_gpu_train.c:74-75 uses hi = V-1)."""
+    r = pcg_stream(seed_a, seed_b)
+    hi = V - 1 if hi_exclusive is None else hi_exclusive
+    f = lib().or_pcg_range_i64
+    return np.array([f(C.byref(r), 0, hi) for _ in range(n)], np.uint32)
+
+
+def gaussian_array(n, seed_a, seed_b, std=1.0):
+    r = pcg_stream(seed_a, seed_b)
+    f = lib().or_pcg_gaussian
+    return np.array([f(C.byref(r), 0.0, std) for _ in range(n)], np.float32)
+
+
+def adam_step(p, g, m, v, t, lr, b1, b2, eps, wd=0.0, grad_scale=1.0):
+    """In-place Adam/AdamW step; t is the step count after increment."""
+    lib().or_adam_step(p, g, m, v, p.size, t, lr, b1, b2, eps, wd, grad_scale)
+
+
+class RefCfg(Cfg):
+    pass
+
+
+class Reference:
+    """The reference's own CPU path (oracle/_ref), when it was built here."""
+
+    def __init__(self):
+        if not (os.path.exists(REF_LIB) and os.path.exists(REF_HARNESS)):
+            raise FileNotFoundError("oracle/_ref not built")
+        self.h = C.CDLL(REF_HARNESS)
+        h = self.h
+        h.refh_open.restype = C.c_int
+        h.refh_open.argtypes = [C.c_char_p]
+        rc = h.refh_open(REF_LIB.encode())
+        if rc != 0:
+            raise RuntimeError("refh_open failed: %d" % rc)
+        cfgp = C.POINTER(Cfg)
+        h.refh_m.restype = C.c_double
+        h.refh_m.argtypes = [C.c_int, C.c_double, C.c_double]
+        h.refh_pcg_u32.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, u32p]
+        h.refh_pcg_range.argtypes = [C.c_uint64, C.c_uint64, C.c_int64, C.c_int64, C.c_uint32, i64p]
+        h.refh_pcg_gauss.argtypes = [C.c_uint64, C.c_uint64, C.c_uint32, f64p]
+        h.refh_rope_tables.argtypes = [C.c_uint32, C.c_uint32, f32p, f32p]
+        h.refh_lm_init.argtypes = [cfgp, C.c_uint64, C.c_uint64, f32p]
+        h.refh_forward_logits.argtypes = [cfgp, f32p, u32p, C.c_uint32, C.c_uint32, f32p, C.c_int]
+        h.refh_forward_backward.restype = C.c_float
+        h.refh_forward_backward.argtypes = [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32,
+                                            C.c_uint64, C.c_void_p, C.c_void_p, C.c_int]
+        h.refh_adam_step.argtypes = [cfgp, f32p, f32p, f32p, f32p, C.c_uint64, C.c_float,
+                                     C.c_float, C.c_float, C.c_float]
+        h.refh_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
+        h.refh_time_train_step.restype = C.c_double
+        h.refh_time_train_step.argtypes = [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32,
+                                           C.c_uint64, f32p, f32p, C.c_int]
+        h.refh_time_forward.restype = C.c_double
+        h.refh_time_forward.argtypes = [cfgp, f32p, u32p, C.c_uint32, C.c_uint32, f32p, C.c_int]
+        h.refh_time_matmul.restype = C.c_double
+        h.refh_time_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
+
+    def lm_init(self, model, seed_a=1337, seed_b=1):
+        p = np.zeros(model.total, np.float32)
+        self.h.refh_lm_init(C.byref(model.cfg), seed_a, seed_b, p)
+        return p
+
+    def forward_logits(self, model, params, ids, B, T, nthreads=None):
+        out = np.zeros((B * T, model.V), np.float32)
+        self.h.refh_forward_logits(C.byref(model.cfg), params, np.ascontiguousarray(ids, np.uint32),
+                                   B, T, out, nthreads or _threads())
+        return out
+
+    def forward_backward(self, model, params, ids, tgt, B, T, nthreads=None):
+        grads = np.zeros(model.total, np.float32)
+        scratch = np.zeros(model.total * B, np.float32)
+        loss = self.h.refh_forward_backward(C.byref(model.cfg), params, np.ascontiguousarray(ids, np.uint32),
+                                            np.ascontiguousarray(tgt, np.uint32), B, T, model.total,
+                                            grads.ctypes.data, scratch.ctypes.data, nthreads or _threads())
+        return np.float32(loss), grads
+
+    def adam_step(self, model, p, g, m, v, t_before, lr, b1, b2, eps):
+        self.h.refh_adam_step(C.byref(model.cfg), p, g, m, v, t_before, lr, b1, b2, eps)
+
+    def matmul(self, A, B):
+        A = np.ascontiguousarray(A, np.float32)
+        B = np.ascontiguousarray(B, np.float32)
+        out = np.zeros((A.shape[0], B.shape[1]), np.float32)
+        self.h.refh_matmul(A.shape[0], B.shape[1], A.shape[1], A, B, out)
+        return out
+
+
+def reference_available():
+    return os.path.exists(REF_LIB) and os.path.exists(REF_HARNESS)

@@ -1,0 +1,97 @@
+"""Forward-only entry points: logits, mean cross-entropy without destroying
+the logits, and greedy argmax (BASELINE configs 1 and 3; additive API).
+
+Config 1 is the reference's own CPU-runnable case: the real architecture,
+lm_init(pcg_seed(1337,1)), B=1, T=128, ids pcg_range_i64(0, 31769) from
+pcg_seed(4242,7).  Logits within 1e-4 of max|logits|; the GPU argmax kernel
+must equal the host argmax of the same logits bit for bit (first index of
+the maximum), and the oracle's next token whenever its top-2 margin exceeds
+the logit tolerance.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def real_model(trlm, orc):
+    model = orc.Model(31769, 384, 6, 12, 1024)
+    params = model.init(1337, 1)
+    hm = trlm.HostModel(31769, 384, 6, 12, 1024, params)
+    yield model, params, hm
+    hm.close()
+
+
+def host_argmax(logits):
+    return np.argmax(logits, axis=1).astype(np.uint32)   # first index of the max
+
+
+def test_config1_logits_and_greedy(trlm, orc, real_model):
+    model, params, hm = real_model
+    ids = orc.random_tokens(128, 31769, 4242, 7, hi_exclusive=31769)
+    want = model.forward_logits(params, ids, 1, 128)
+    tr = trlm.Trainer(hm, 1, 128)
+    try:
+        got = tr.forward_logits(ids)
+        am = tr.greedy_argmax()
+    finally:
+        tr.destroy()
+    scale = np.abs(want).max()
+    err = np.abs(got.astype(np.float64) - want).max() / scale
+    assert err <= 1e-4, err
+    assert np.array_equal(am, host_argmax(got))
+    ref_next = host_argmax(want)
+    top2 = np.sort(want, axis=1)[:, -2:]
+    clear = (top2[:, 1] - top2[:, 0]) > 4e-4 * scale
+    assert np.array_equal(am[clear], ref_next[clear])
+    print("config1: logits rel err %.3e, next token %d (oracle %d)" % (err, am[-1], ref_next[-1]))
+
+
+@pytest.mark.parametrize("V,D,H,L,F,T,B", [(50, 32, 2, 2, 48, 12, 5), (500, 64, 2, 2, 128, 256, 3)])
+def test_forward_loss_keeps_logits(trlm, orc, V, D, H, L, F, T, B):
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    toks = orc.random_tokens(8000, V)
+    ids, tgt = orc.sample_batch(toks, T, B, 77)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, B, T)
+    try:
+        loss, logits = tr.forward_loss_logits(ids, tgt)
+        ev = tr.eval_loss(ids, tgt)
+        logits2 = tr.forward_logits(ids)
+        am = tr.greedy_argmax()
+    finally:
+        tr.destroy()
+        hm.close()
+    want = model.forward_logits(params, ids, B, T)
+    cpu_loss, _, _ = model.forward_backward(params, ids, tgt, B, T, want_grads=False)
+    assert np.float32(loss).view(np.uint32) == np.float32(ev).view(np.uint32)
+    assert abs(loss - cpu_loss) <= 1e-4 * abs(cpu_loss)
+    assert np.array_equal(logits.view(np.uint32), logits2.view(np.uint32))
+    assert np.abs(logits - want).max() <= 1e-4 * np.abs(want).max()
+    assert np.array_equal(am, host_argmax(logits2))
+
+
+def test_argmax_ties_pick_lowest_index(trlm):
+    """Rows with repeated maxima: the kernel must return the first index."""
+    _, hip = trlm.libs()
+    import ctypes as C
+    dev = trlm.Device()
+    try:
+        rows, V = 7, 1000
+        z = np.zeros((rows, V), np.float32)
+        spots = [(0, [5, 900]), (1, [0, 999]), (2, [255, 256, 511]), (3, [998, 999]), (4, [10]), (5, [700, 3]),
+                 (6, list(range(0, 1000, 37)))]
+        for r, cols in spots:
+            z[r, cols] = 3.0
+        dz, dout = dev.upload(z), dev.empty(rows * 4)
+        f = hip.hip_get_kernel(C.byref(dev.ctx), b"k_argmax_rows")
+        pz, po = C.c_void_p(dz), C.c_void_p(dout)
+        ld, vv = C.c_int32(V), C.c_int32(V)
+        args = (C.c_void_p * 4)(C.addressof(pz), C.addressof(ld), C.addressof(vv), C.addressof(po))
+        hip.hip_launch(f, rows, 1, 1, 256, 1, 1, 0, args)
+        out = dev.download(dout, rows, np.uint32)
+        assert list(out) == [min(c) for _, c in spots]
+    finally:
+        dev.close()

@@ -1,0 +1,218 @@
+"""fp32 MFMA GEMM parity through the C ABI (trlm_gemm), against fp64 numpy.
+
+Covers the reference's GEMM contract (train_kernels.cu:97-193,226-329;
+gpu_train.c:42-118): NN / NT / TN layouts, batched strides, alpha/beta,
+bias and residual epilogues, off-grid shapes (M, N, K not multiples of the
+tiles), unaligned leading dimensions (scalar-load variants), split-K, and the
+model's real shapes at M = B*T = 8192.  Tolerance: max |C - C64| <= 1e-4 *
+max |C64| per output (the north star's fp32 bar), except exact cases.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev(trlm):
+    d = trlm.Device()
+    yield d
+    d.close()
+
+
+def stored(op_mat, trans):
+    """The array as it is stored for a given op(): A^T is stored for trans."""
+    return np.ascontiguousarray(op_mat.T if trans else op_mat)
+
+
+def run_gemm(dev, A, B, ta, tb, alpha=1.0, beta=0.0, C0=None, bias=None, resid=None, pad=0):
+    """C = alpha*A@B (+beta*C0) (+bias) (+resid) with A [M,K], B [K,N] given as
+    op() values; stored transposed when ta/tb.  pad widens leading dims."""
+    M, K = A.shape
+    N = B.shape[1]
+    As, Bs = stored(A, ta), stored(B, tb)
+    if pad:
+        As = np.pad(As, ((0, 0), (0, pad)))
+        Bs = np.pad(Bs, ((0, 0), (0, pad)))
+    lda, ldb = As.shape[1], Bs.shape[1]
+    dA, dB = dev.upload(As.astype(np.float32)), dev.upload(Bs.astype(np.float32))
+    c_init = np.zeros((M, N), np.float32) if C0 is None else C0.astype(np.float32)
+    dC = dev.upload(c_init)
+    dbias = dev.upload(bias.astype(np.float32)) if bias is not None else None
+    dres = dev.upload(resid.astype(np.float32)) if resid is not None else None
+    dev.matmul(ta, tb, dA, dB, dC, M, N, K, lda, ldb, N, alpha=alpha, beta=beta, bias=dbias, resid=dres, ldr=N)
+    out = dev.download(dC, (M, N))
+    variant = dev.last_variant()
+    for p in (dA, dB, dC, dbias, dres):
+        if p is not None:
+            dev.free(p)
+    return out, variant
+
+
+def ref64(A, B, alpha=1.0, beta=0.0, C0=None, bias=None, resid=None):
+    r = alpha * (A.astype(np.float64) @ B.astype(np.float64))
+    if beta != 0.0:
+        r = r + beta * C0
+    if bias is not None:
+        r = r + bias
+    if resid is not None:
+        r = resid + r
+    return r
+
+
+def close(got, want, tol=1e-4):
+    scale = max(np.abs(want).max(), 1e-30)
+    err = np.abs(got.astype(np.float64) - want).max()
+    return err <= tol * scale, err / scale
+
+
+def test_mfma_lane_layout(trlm, dev):
+    """The operand/result lane layout every GEMM and attention kernel
+    assumes for v_mfma_f32_32x32x2f32, checked exactly with small integers."""
+    hip = dev.hip
+    rng = np.random.default_rng(0)
+    a = rng.integers(-4, 5, 64).astype(np.float32)
+    b = rng.integers(-4, 5, 64).astype(np.float32)
+    da, db, dout = dev.upload(a), dev.upload(b), dev.empty(64 * 16 * 4)
+    f = hip.hip_get_kernel(C.byref(dev.ctx), b"k_mfma_layout_probe")
+    pa, pb, po = C.c_void_p(da), C.c_void_p(db), C.c_void_p(dout)
+    args = (C.c_void_p * 3)(C.addressof(pa), C.addressof(pb), C.addressof(po))
+    hip.hip_launch(f, 1, 1, 1, 64, 1, 1, 0, args)
+    out = dev.download(dout, (64, 16))
+    A = np.zeros((32, 2)); B = np.zeros((2, 32))
+    for l in range(64):
+        A[l % 32, l // 32] = a[l]
+        B[l // 32, l % 32] = b[l]
+    D = A @ B
+    want = np.zeros((64, 16))
+    for l in range(64):
+        for r in range(16):
+            want[l, r] = D[8 * (r // 4) + 4 * (l // 32) + r % 4, l % 32]
+    for p in (da, db, dout):
+        dev.free(p)
+    assert np.array_equal(out, want)
+
+
+SMALL = [  # M, N, K
+    (1, 1, 1), (4, 5, 3), (12, 150, 32), (65, 33, 17), (64, 64, 64), (127, 129, 130),
+    (200, 96, 48), (31, 1000, 40), (128, 128, 16), (300, 200, 600), (96, 160, 1200),
+]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0), (1, 1)])
+@pytest.mark.parametrize("M,N,K", SMALL)
+def test_gemm_offgrid(dev, M, N, K, ta, tb):
+    rng = np.random.default_rng(M * 7 + N * 13 + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    got, var = run_gemm(dev, A, B, ta, tb)
+    ok, rel = close(got, ref64(A, B))
+    assert ok, (var, rel)
+
+
+def test_gemm_small_integers_exact(dev):
+    """test_cuda.c:55-94's case (4x3 @ 3x5 of small exact values): exact."""
+    A = np.array([(i % 7) - 3.0 for i in range(12)], np.float32).reshape(4, 3)
+    B = np.array([(i % 5) * 0.5 for i in range(15)], np.float32).reshape(3, 5)
+    for ta, tb in [(0, 0), (0, 1), (1, 0)]:
+        got, _ = run_gemm(dev, A, B, ta, tb)
+        assert np.array_equal(got, (A.astype(np.float64) @ B).astype(np.float32))
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_gemm_epilogue(dev, ta, tb):
+    rng = np.random.default_rng(5)
+    M, N, K = 257, 190, 96
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    got, _ = run_gemm(dev, A, B, ta, tb, alpha=0.5, beta=1.0, C0=C0, bias=bias, resid=resid)
+    ok, rel = close(got, ref64(A, B, 0.5, 1.0, C0, bias, resid))
+    assert ok, rel
+
+
+def test_gemm_unaligned_leading_dims(dev):
+    rng = np.random.default_rng(9)
+    M, N, K = 71, 45, 33   # with pad=2 every stored row length is odd
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    for ta, tb in [(0, 0), (0, 1), (1, 0)]:
+        got, var = run_gemm(dev, A, B, ta, tb, pad=2)
+        assert var[0].endswith("_u")
+        ok, rel = close(got, ref64(A, B))
+        assert ok, (var, rel)
+
+
+@pytest.mark.parametrize("M,N,K", [(384, 384, 8192), (100, 68, 4000), (1024, 384, 8192), (700, 132, 2048)])
+def test_gemm_split_k(dev, M, N, K):
+    """Long-K weight-gradient shapes take the split-K path; partials are
+    reduced in split order, so two runs are bit-identical."""
+    rng = np.random.default_rng(M + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    got, var = run_gemm(dev, A, B, 1, 0)
+    assert var[1] > 1, var
+    ok, rel = close(got, ref64(A, B))
+    assert ok, (var, rel)
+    again, _ = run_gemm(dev, A, B, 1, 0)
+    assert np.array_equal(got.view(np.uint32), again.view(np.uint32))
+
+
+def test_gemm_batched(dev):
+    rng = np.random.default_rng(11)
+    bt, M, N, K = 5, 70, 50, 40
+    A = rng.standard_normal((bt, M, K)).astype(np.float32)
+    B = rng.standard_normal((bt, K, N)).astype(np.float32)
+    dA, dB, dC = dev.upload(A), dev.upload(B), dev.empty(bt * M * N * 4)
+    dev.matmul(0, 0, dA, dB, dC, M, N, K, K, N, N, batch=bt, sA=M * K, sB=K * N, sC=M * N)
+    got = dev.download(dC, (bt, M, N))
+    for p in (dA, dB, dC):
+        dev.free(p)
+    want = np.einsum("bmk,bkn->bmn", A.astype(np.float64), B.astype(np.float64))
+    ok, rel = close(got, want)
+    assert ok, rel
+
+
+MODEL = [  # name, M, N, K, ta, tb (row-major as the trainer lays them out)
+    ("qkv_fwd", 8192, 1152, 384, 0, 0),
+    ("attn_out_fwd", 8192, 384, 384, 0, 0),
+    ("gate_up_fwd", 8192, 2048, 384, 0, 0),
+    ("down_fwd", 8192, 384, 1024, 0, 0),
+    ("qkv_dx", 8192, 384, 1152, 0, 1),
+    ("down_dx", 8192, 1024, 384, 0, 1),
+    ("qkv_dw", 384, 1152, 8192, 1, 0),
+    ("gate_up_dw", 384, 2048, 8192, 1, 0),
+    ("down_dw", 1024, 384, 8192, 1, 0),
+]
+
+
+@pytest.mark.parametrize("name,M,N,K,ta,tb", MODEL)
+def test_gemm_model_shapes(dev, name, M, N, K, ta, tb):
+    rng = np.random.default_rng(len(name))
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
+    got, var = run_gemm(dev, A, B, ta, tb)
+    ok, rel = close(got, ref64(A, B))
+    assert ok, (name, var, rel)
+
+
+def test_gemm_lm_head_rows(dev):
+    """LM head NT [8192,384] x E[31769,384]^T, checked on a row sample."""
+    rng = np.random.default_rng(3)
+    M, N, K = 8192, 31769, 384
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    E = (0.02 * rng.standard_normal((N, K))).astype(np.float32)
+    ldc = (N + 3) // 4 * 4
+    dA, dE, dC = dev.upload(A), dev.upload(E), dev.empty(M * ldc * 4)
+    dev.matmul(0, 1, dA, dE, dC, M, N, K, K, K, ldc)
+    got = dev.download(dC, (M, ldc))[:, :N]
+    for p in (dA, dE, dC):
+        dev.free(p)
+    rows = rng.choice(M, 64, replace=False)
+    want = A[rows].astype(np.float64) @ E.T.astype(np.float64)
+    ok, rel = close(got[rows], want)
+    assert ok, rel

@@ -1,0 +1,196 @@
+"""GPU trainer vs the CPU oracle on identical seeded inputs -- the
+assertions of the reference's tests/test_gpu_train.c, at a 1e-4 bar.
+
+Cases (test_gpu_train.c:261-271): small shapes off every tile grid
+(V50 D32 H2 L2 F48 T12 B5), long context (V500 D64 H2 L2 F128 T1024 B2),
+and the real model (V31769 D384 H6 L12 F1024 T128 B4).  Inputs exactly as
+the reference test builds them: weights lm_init(pcg_seed(1337,1)), tokens
+pcg_range_i64(0, V-1) from pcg_seed(4242,7), batch seed 2026.
+
+Checks per case:
+  loss within 1e-4 relative; every gradient tensor within
+  1e-4*max|want| + 1e-4*|want| (compare_tensor, test_gpu_train.c:53-66);
+  bit-identical rerun; eval_loss == forward_backward loss bit for bit;
+  grad norm vs f64 host norm (< 1e-5) and repeatable; Adam vs the CPU Adam
+  on identical gradients; upload/download lossless; adam_step_scaled(0.5,G)
+  == adam_step(0.5*G) bit for bit; AdamW(wd=0) == Adam bit for bit.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "small_offgrid": dict(V=50, D=32, H=2, L=2, F=48, T=12, B=5, ntok=4000),
+    "long_context": dict(V=500, D=64, H=2, L=2, F=128, T=1024, B=2, ntok=20000),
+    "real_scale": dict(V=31769, D=384, H=6, L=12, F=1024, T=128, B=4, ntok=200000),
+}
+TOL = 1e-4
+
+
+def compare_tensor(got, want, rel_tol):
+    maxabs = float(np.abs(want).max()) if want.size else 0.0
+    floor = maxabs * rel_tol + 1e-12
+    diff = np.abs(got.astype(np.float64) - want.astype(np.float64))
+    bad = int((diff > floor + rel_tol * np.abs(want)).sum())
+    worst = float(diff.max() / (maxabs + 1e-30)) if want.size else 0.0
+    return bad, worst
+
+
+@pytest.fixture(scope="module", params=list(CASES))
+def case(request, trlm, orc):
+    c = CASES[request.param]
+    model = orc.Model(c["V"], c["D"], c["H"], c["L"], c["F"])
+    params = model.init(1337, 1)
+    tokens = orc.random_tokens(c["ntok"], c["V"])
+    ids, tgt = orc.sample_batch(tokens, c["T"], c["B"], 2026)
+    loss, grads, rows = model.forward_backward(params, ids, tgt, c["B"], c["T"])
+    hm = trlm.HostModel(c["V"], c["D"], c["H"], c["L"], c["F"], params)
+    tr = trlm.Trainer(hm, c["B"], c["T"])
+    yield dict(name=request.param, cfg=c, model=model, params=params, tokens=tokens, ids=ids, tgt=tgt,
+               loss=loss, grads=grads, hm=hm, tr=tr)
+    tr.destroy()
+    hm.close()
+
+
+def test_sample_batch_matches(case, trlm):
+    c = case["cfg"]
+    _, hip = trlm.libs()
+    ids = np.zeros(c["B"] * c["T"], np.uint32)
+    tgt = np.zeros_like(ids)
+    hip.gpu_trainer_sample_batch(case["tokens"], len(case["tokens"]), c["T"], c["B"], 2026, ids, tgt)
+    assert np.array_equal(ids, case["ids"]) and np.array_equal(tgt, case["tgt"])
+
+
+def _reset(case):
+    case["hm"].set_values(case["params"])
+    case["tr"].upload()
+
+
+def test_loss_and_grads(case):
+    tr, model = case["tr"], case["model"]
+    _reset(case)
+    loss = tr.forward_backward(case["ids"], case["tgt"])
+    assert abs(loss - case["loss"]) <= TOL * abs(case["loss"]), (loss, case["loss"])
+    got = tr.grads()
+    failures = []
+    worst_all = 0.0
+    for i, (g, w) in enumerate(zip(model.split(got), model.split(case["grads"]))):
+        bad, worst = compare_tensor(g, w, TOL)
+        worst_all = max(worst_all, worst)
+        if bad:
+            failures.append((i, bad, w.size, worst))
+    print("%s: loss gpu=%.7f cpu=%.7f worst rel grad err %.3e" % (case["name"], loss, case["loss"], worst_all))
+    assert not failures, failures
+
+
+def test_determinism_and_eval(case):
+    tr = case["tr"]
+    _reset(case)
+    l1 = np.float32(tr.forward_backward(case["ids"], case["tgt"]))
+    g1 = tr.grads()
+    l2 = np.float32(tr.forward_backward(case["ids"], case["tgt"]))
+    g2 = tr.grads()
+    assert l1.view(np.uint32) == l2.view(np.uint32)
+    assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+    ev = np.float32(tr.eval_loss(case["ids"], case["tgt"]))
+    assert ev.view(np.uint32) == l2.view(np.uint32)
+
+
+def test_grad_norm(case):
+    tr = case["tr"]
+    _reset(case)
+    tr.forward_backward(case["ids"], case["tgt"])
+    g = tr.grads()
+    cpu = float(np.sqrt(np.sum(g.astype(np.float64) ** 2)))
+    n1 = tr.grad_norm()
+    n2 = tr.grad_norm()
+    assert abs(n1 - cpu) / cpu < 1e-5
+    assert n1 == n2
+
+
+def test_adam_matches_cpu(case, trlm, orc):
+    """CPU Adam (adam.c) and GPU Adam from identical gradients
+    (test_gpu_train.c:176-203); Adam's update rounds the same way on both
+    sides, so the result is also compared bit for bit."""
+    tr, hm = case["tr"], case["hm"]
+    params, grads = case["params"], case["grads"]
+    hm.set_values(params)
+    adam = trlm.Adam(hm, 3e-4, 0.9, 0.999, 1e-8)
+    tr.upload(adam)
+    tr.upload_grads(grads)
+    tr.adam_step(adam)
+    got = tr.download(adam)
+    assert adam.opt.t == 1
+    p = params.copy(); m = np.zeros_like(p); v = np.zeros_like(p)
+    orc.adam_step(p, grads, m, v, 1, 3e-4, 0.9, 0.999, 1e-8)
+    tol = 1e-3 * 3e-4 + 1e-6 * np.abs(p)
+    assert int((np.abs(got - p) > tol).sum()) == 0
+    assert np.array_equal(adam.flat("m"), m) and np.array_equal(adam.flat("v"), v)
+    print("%s: adam bit-identical elements %.6f" % (case["name"], np.mean(got.view(np.uint32) == p.view(np.uint32))))
+
+
+def test_upload_download_roundtrip(case, trlm):
+    tr, hm = case["tr"], case["hm"]
+    rng = np.random.default_rng(1)
+    vals = rng.standard_normal(hm.total).astype(np.float32)
+    hm.set_values(vals)
+    adam = trlm.Adam(hm)
+    adam.set_flat("m", vals * 0.5)
+    adam.set_flat("v", np.abs(vals))
+    tr.upload(adam)
+    hm.set_values(np.zeros_like(vals))
+    adam.set_flat("m", np.zeros_like(vals)); adam.set_flat("v", np.zeros_like(vals))
+    back = tr.download(adam)
+    assert np.array_equal(back.view(np.uint32), vals.view(np.uint32))
+    assert np.array_equal(adam.flat("m"), vals * 0.5) and np.array_equal(adam.flat("v"), np.abs(vals))
+
+
+def _adam_from(tr, hm, trlm, params, m, v, t, grads, scale=None, wd=None):
+    hm.set_values(params)
+    adam = trlm.Adam(hm)
+    adam.set_flat("m", m); adam.set_flat("v", v)
+    adam.opt.t = t
+    tr.upload(adam)
+    tr.upload_grads(grads)
+    if wd is not None:
+        tr.adamw_step(adam, wd, 1.0 if scale is None else scale)
+    else:
+        tr.adam_step(adam, scale)
+    return tr.download(adam), adam.flat("m"), adam.flat("v")
+
+
+def test_adam_scaled_equals_prescaled(case, trlm):
+    """adam_step_scaled(0.5, G) == adam_step(0.5*G) bit for bit
+    (test_gpu_train.c:214-250)."""
+    tr, hm = case["tr"], case["hm"]
+    rng = np.random.default_rng(2)
+    p = case["params"]
+    m = (1e-3 * rng.standard_normal(p.size)).astype(np.float32)
+    v = (1e-6 * rng.random(p.size)).astype(np.float32)
+    G = case["grads"]
+    a = _adam_from(tr, hm, trlm, p, m, v, 3, 0.5 * G)
+    b = _adam_from(tr, hm, trlm, p, m, v, 3, G, scale=0.5)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+
+
+def test_adamw(case, trlm, orc):
+    """AdamW with wd = 0 is Adam bit for bit; wd = 0.1 (betas 0.9/0.95, the
+    training configuration) matches the closed form on identical inputs."""
+    tr, hm = case["tr"], case["hm"]
+    p, G = case["params"], case["grads"]
+    z = np.zeros_like(p)
+    a = _adam_from(tr, hm, trlm, p, z, z, 0, G)
+    b = _adam_from(tr, hm, trlm, p, z, z, 0, G, wd=0.0)
+    for x, y in zip(a, b):
+        assert np.array_equal(x.view(np.uint32), y.view(np.uint32))
+    hm.set_values(p)
+    adam = trlm.Adam(hm, 3e-4, 0.9, 0.95, 1e-8)
+    tr.upload(adam)
+    tr.upload_grads(G)
+    tr.adamw_step(adam, 0.1)
+    got = tr.download(adam)
+    want = p.copy(); m = np.zeros_like(p); v = np.zeros_like(p)
+    orc.adam_step(want, G, m, v, 1, 3e-4, 0.9, 0.95, 1e-8, 0.1)
+    assert int((np.abs(got - want) > 1e-3 * 3e-4 + 1e-6 * np.abs(want)).sum()) == 0

@@ -1,0 +1,206 @@
+/* gpu_ops.c -- node_matmul2d_gpu on the MFMA GEMM (see include/gpu_ops.h).
+ *
+ * Same contract as the reference's model/gpu_ops.c: an autograd node whose
+ * forward A@B and backward dA += dC@B^T, dB += A^T@dC run on the GPU, with
+ * host round-trips by API design and gradient accumulation on the host
+ * (gpu_ops.c:224-235).  Differences, all MI355X-side:
+ *   - an operand that is a transposed view of a contiguous tensor (the tied
+ *     head's embed_table^T, every B^T / A^T of the backward) is uploaded as
+ *     stored and handed to the GEMM as a transposed layout; the reference
+ *     makes a contiguous host copy first (gpu_ops.c:182-183);
+ *   - row-major views with a wider row stride (column slices) are uploaded
+ *     with one pitched copy and used with their leading dimension;
+ *   - each slot owns a stream and grow-only device buffers (as the
+ *     reference's persistent buffers, gpu_ops.c:85-108).
+ */
+#include <pthread.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include <time.h>
+#include <unistd.h>
+
+#include "gpu_ops.h"
+#include "trlm_ext.h"
+
+#define MAX_GPU_CONTEXTS 32
+
+typedef struct Slot {
+    HipCtx ctx;
+    TrlmGemm* gemm;
+    hipDeviceptr_t buf[3];
+    u64 cap[3];
+} Slot;
+
+static Slot g_slots[MAX_GPU_CONTEXTS];
+static u32 g_num_worker_slots = 0;
+static int g_initialized = 0;
+static pthread_mutex_t g_slot0_mutex = PTHREAD_MUTEX_INITIALIZER;
+static pthread_mutex_t g_debug_mutex = PTHREAD_MUTEX_INITIALIZER;
+static _Thread_local i32 g_tls_worker_id = -1;
+static f64 g_debug_seconds = 0.0;
+static u32 g_debug_calls = 0;
+
+static f64 now_seconds(void) {
+    struct timespec ts;
+    clock_gettime(CLOCK_MONOTONIC, &ts);
+    return (f64)ts.tv_sec + (f64)ts.tv_nsec * 1e-9;
+}
+
+void gpu_ops_debug_stats(f64* out_total_seconds, u32* out_call_count) {
+    pthread_mutex_lock(&g_debug_mutex);
+    *out_total_seconds = g_debug_seconds;
+    *out_call_count = g_debug_calls;
+    pthread_mutex_unlock(&g_debug_mutex);
+}
+
+void gpu_ops_debug_reset(void) {
+    pthread_mutex_lock(&g_debug_mutex);
+    g_debug_seconds = 0.0;
+    g_debug_calls = 0;
+    pthread_mutex_unlock(&g_debug_mutex);
+}
+
+static void slot_init(u32 s, Allocator* scratch, const char* path, i32 device) {
+    memset(&g_slots[s], 0, sizeof(Slot));
+    g_slots[s].ctx = hip_init_on_device(scratch, path, device);
+    hip_set_current(&g_slots[s].ctx);
+    g_slots[s].gemm = trlm_gemm_create(&g_slots[s].ctx);
+}
+
+void gpu_ops_init(Allocator* scratch, const char* ptx_path) {
+    slot_init(0, scratch, ptx_path, 0);
+    g_initialized = 1;
+}
+
+/* One slot per worker, spread round-robin over the visible devices
+ * (gpu_ops.c:140-160). */
+void gpu_ops_init_workers(Allocator* scratch, const char* ptx_path, u32 num_workers) {
+    if (num_workers > MAX_GPU_CONTEXTS - 1) num_workers = MAX_GPU_CONTEXTS - 1;
+    i32 ndev = hip_device_count();
+    if (ndev < 1) ndev = 1;
+    for (u32 i = 0; i < num_workers; i++) slot_init(1 + i, scratch, ptx_path, (i32)(i % (u32)ndev));
+    g_num_worker_slots = num_workers;
+}
+
+void gpu_ops_set_worker_id(i32 worker_id) { g_tls_worker_id = worker_id; }
+
+static void slot_release(u32 s) {
+    hip_set_current(&g_slots[s].ctx);
+    trlm_gemm_destroy(g_slots[s].gemm);
+    g_slots[s].gemm = NULL;
+    hip_shutdown(&g_slots[s].ctx);
+}
+
+void gpu_ops_shutdown(void) {
+    if (!g_initialized) return;
+    slot_release(0);
+    for (u32 i = 0; i < g_num_worker_slots; i++) slot_release(1 + i);
+    g_num_worker_slots = 0;
+    g_initialized = 0;
+}
+
+static hipDeviceptr_t slot_buf(Slot* s, u32 which, u64 bytes) {
+    if (s->cap[which] < bytes) {
+        if (s->cap[which] > 0) hip_free(s->buf[which]);
+        s->buf[which] = hip_alloc(bytes);
+        s->cap[which] = bytes;
+    }
+    return s->buf[which];
+}
+
+/* How a 2-D view is laid out in host memory. */
+typedef struct View {
+    int trans;          /* 0: element (r,c) at data[r*ld + c]; 1: at data[c*ld + r] */
+    u64 ld;
+    const f32* data;
+    Tensor packed;      /* host copy when the view has neither form */
+} View;
+
+static View classify(Allocator* alloc, const Tensor* t) {
+    View v;
+    memset(&v, 0, sizeof(v));
+    u64 rows = t->shape[0], cols = t->shape[1];
+    if (t->strides[1] == 1 && (u64)t->strides[0] >= cols) {
+        v.trans = 0; v.ld = (u64)t->strides[0]; v.data = t->data;
+    } else if (t->strides[0] == 1 && (u64)t->strides[1] >= rows) {
+        v.trans = 1; v.ld = (u64)t->strides[1]; v.data = t->data;
+    } else {
+        v.packed = tensor_contiguous(alloc, t);
+        v.trans = 0; v.ld = cols; v.data = v.packed.data;
+    }
+    if (rows <= 1 && !v.trans) v.ld = cols;
+    if (cols <= 1 && v.trans) v.ld = rows;
+    return v;
+}
+
+/* Upload a view into a packed device buffer (leading dimension = its stored
+ * row length) and return that leading dimension. */
+static u64 upload_view(Slot* s, u32 which, const View* v, u64 rows, u64 cols) {
+    u64 srow = v->trans ? rows : cols;      /* stored row length */
+    u64 nrow = v->trans ? cols : rows;      /* stored row count  */
+    hipDeviceptr_t d = slot_buf(s, which, nrow * srow * sizeof(f32));
+    if (v->ld == srow) {
+        hip_h2d(d, v->data, nrow * srow * sizeof(f32));
+    } else {
+        hipError_t r = hipMemcpy2DAsync(d, srow * sizeof(f32), v->data, v->ld * sizeof(f32), srow * sizeof(f32),
+                                        nrow, hipMemcpyHostToDevice, s->ctx.stream);
+        if (r != hipSuccess) {
+            fprintf(stderr, "[HIP ERROR] gpu_ops: pitched upload -> %s\n", hipGetErrorName(r));
+            _exit(1);
+        }
+        hip_sync();
+    }
+    return srow;
+}
+
+static Tensor gpu_matmul(Allocator* alloc, const Tensor* a, const Tensor* b) {
+    f64 t0 = now_seconds();
+    u64 M = a->shape[0], K = a->shape[1], N = b->shape[1];
+    u64 out_shape[2] = { M, N };
+    Tensor out = tensor_create(alloc, out_shape, 2);
+    View va = classify(alloc, a), vb = classify(alloc, b);
+
+    i32 wid = g_tls_worker_id;
+    int own = (wid >= 0 && (u32)wid < g_num_worker_slots);
+    u32 slot = own ? (u32)(1 + wid) : 0;
+    if (!own) pthread_mutex_lock(&g_slot0_mutex);
+    Slot* s = &g_slots[slot];
+    hip_set_current(&s->ctx);
+
+    u64 lda = upload_view(s, 0, &va, M, K);
+    u64 ldb = upload_view(s, 1, &vb, K, N);
+    hipDeviceptr_t dc = slot_buf(s, 2, (M * N > 0 ? M * N : 1) * sizeof(f32));
+    trlm_gemm(s->gemm, va.trans, vb.trans, s->buf[0], s->buf[1], dc, (i32)M, (i32)N, (i32)K, (i32)lda, (i32)ldb,
+              (i32)N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, (i32)N);
+    hip_d2h(out.data, dc, M * N * sizeof(f32));
+
+    if (!own) pthread_mutex_unlock(&g_slot0_mutex);
+    pthread_mutex_lock(&g_debug_mutex);
+    g_debug_seconds += now_seconds() - t0;
+    g_debug_calls++;
+    pthread_mutex_unlock(&g_debug_mutex);
+    return out;
+}
+
+/* dA += dC @ B^T ; dB += A^T @ dC  (gpu_ops.c:224-235) */
+static void backward_matmul2d_gpu(Node* self, Allocator* alloc) {
+    Node* a = self->parents[0];
+    Node* b = self->parents[1];
+    Tensor bt = tensor_transpose(&b->value, 0, 1);
+    Tensor da = gpu_matmul(alloc, &self->grad, &bt);
+    tensor_add_inplace(&a->grad, &da);
+    Tensor at = tensor_transpose(&a->value, 0, 1);
+    Tensor db = gpu_matmul(alloc, &at, &self->grad);
+    tensor_add_inplace(&b->grad, &db);
+}
+
+Node* node_matmul2d_gpu(Allocator* alloc, Node* a, Node* b) {
+    Tensor v = gpu_matmul(alloc, &a->value, &b->value);
+    Node* n = node_make_custom(alloc, v, TRUE);
+    n->parents[0] = a;
+    n->parents[1] = b;
+    n->num_parents = 2;
+    n->backward_fn = backward_matmul2d_gpu;
+    return n;
+}

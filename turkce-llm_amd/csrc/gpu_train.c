@@ -1,0 +1,569 @@
+/* gpu_train.c -- GPU-resident forward, backward and Adam on MI355X.
+ *
+ * Same API and semantics as the reference's model/gpu_train.c (cited per
+ * function), re-planned for gfx950:
+ *   - every projection and the tied LM head run on the fp32 MFMA GEMM
+ *     (trlm_gemm.c) with bias and residual fused into the epilogue;
+ *   - attention is flash style (attention.hip): no [B,H,T,T] tensor, Q/K/V
+ *     read in place from the qkv projection, O written in place into the
+ *     [N,D] attention output, so the head split/merge passes disappear;
+ *   - bias / norm-weight gradients are two-stage fixed-order column sums and
+ *     the embedding backward is a per-token segmented sum in ascending row
+ *     order, so no reduction uses atomics;
+ *   - one HIP stream per trainer; the blocking points are the reference's
+ *     (loss readback, grad-norm readback, end of the Adam step).
+ */
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+#include "trlm_ext.h"
+
+/* lm_collect_params order (model/gpu_train.c:8-13): [0] embedding; layer l
+ * at 1 + 10*l + k; last = final norm weight. */
+enum { PK_ATTN_NORM = 0, PK_WQKV, PK_BQKV, PK_WO, PK_BO, PK_FFN_NORM, PK_WGU, PK_BGU, PK_WDOWN, PK_BDOWN };
+
+static u32 pidx(u32 layer, u32 k) { return 1u + 10u * layer + k; }
+
+#define F4 ((u64)sizeof(f32))
+
+static hipDeviceptr_t dptr(hipDeviceptr_t base, u64 floats) { return (hipDeviceptr_t)((char*)base + floats * F4); }
+static hipDeviceptr_t P_(const GpuTrainer* g, u32 i) { return dptr(g->params, g->offsets[i]); }
+static hipDeviceptr_t G_(const GpuTrainer* g, u32 i) { return dptr(g->grads, g->offsets[i]); }
+static hipDeviceptr_t dalloc(u64 floats) { return hip_alloc(floats * F4); }
+
+static void fatal(const char* msg) {
+    fprintf(stderr, "[HIP ERROR] gpu_train: %s\n", msg);
+    fflush(stderr);
+    _exit(1);
+}
+
+/* ---------------- launch helpers ---------------- */
+
+static u32 cdiv_u64(u64 a, u64 b) { return (u32)((a + b - 1) / b); }
+
+static void fill_zero(GpuTrainer* g, hipDeviceptr_t p, u64 n) {
+    long long nn = (long long)n;
+    void* args[] = { &p, &nn };
+    u32 grid = cdiv_u64(n, 256);
+    if (grid > 4096) grid = 4096;
+    if (grid == 0) return;
+    hip_launch(g->k.fill_zero, grid, 1, 1, 256, 1, 1, 0, args);
+}
+
+/* C[M,N] = op(A) op(B) (+ beta C) (+ bias) (+ resid), single matrices with
+ * the reference's leading-dimension conventions (gpu_train.c:53-63). */
+typedef enum { GEMM_NN, GEMM_NT, GEMM_TN } GemmKind;
+
+static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C, i32 M, i32 N,
+                  i32 K, i32 lda, i32 ldb, i32 ldc, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid) {
+    trlm_gemm(g->gemm, kind == GEMM_TN, kind == GEMM_NT, A, B, C, M, N, K, lda, ldb, ldc, 1, 0, 0, 0, 1.0f, beta,
+              bias, resid, ldc);
+}
+
+static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv) {
+    i32 rows = (i32)g->N, cols = (i32)g->D;
+    f32 eps = g->eps;
+    void* args[] = { &x, &w, &out, &rinv, &rows, &cols, &eps };
+    hip_launch(g->k.rmsnorm_fwd, cdiv_u64(g->N, 4), 1, 1, 256, 1, 1, 0, args);
+}
+
+#define RMS_ROWS 32u
+
+/* dx += RMSNorm backward; dw = sum over rows of dy*x*r  (gpu_train.c:132-140) */
+static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t rinv, hipDeviceptr_t dy,
+                        hipDeviceptr_t dx, hipDeviceptr_t dw) {
+    i32 rows = (i32)g->N, cols = (i32)g->D;
+    hipDeviceptr_t part = g->part;
+    u32 nb = cdiv_u64(g->N, RMS_ROWS);
+    void* args[] = { &x, &w, &rinv, &dy, &dx, &part, &rows, &cols };
+    hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
+    i32 inb = (i32)nb, acc = 0;
+    void* args2[] = { &part, &inb, &cols, &dw, &acc };
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 256), 1, 1, 256, 1, 1, 0, args2);
+}
+
+#define COLSUM_RPB 64u
+
+/* out[c] = sum_r in[r, c] (bias gradients; the role of colsum_acc,
+ * gpu_train.c:120-123) */
+static void colsum(GpuTrainer* g, hipDeviceptr_t in, hipDeviceptr_t out, i32 rows, i32 cols) {
+    hipDeviceptr_t part = g->part;
+    i32 ld = cols, rpb = (i32)COLSUM_RPB;
+    u32 nb = cdiv_u64((u64)rows, COLSUM_RPB);
+    void* args[] = { &in, &rows, &cols, &ld, &rpb, &part };
+    hip_launch(g->k.colsum_partial, nb, cdiv_u64((u64)cols, 256), 1, 256, 1, 1, 0, args);
+    i32 inb = (i32)nb, acc = 0;
+    void* args2[] = { &part, &inb, &cols, &out, &acc };
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 256), 1, 1, 256, 1, 1, 0, args2);
+}
+
+/* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
+typedef struct AttnParams {
+    const float* qkv;
+    float* out;
+    const float* O;
+    const float* dO;
+    float* lse;
+    float* dvec;
+    int B, T, H, D;
+    int ldq, ldo;
+    float scale;
+} AttnParams;
+
+static AttnParams attn_params(GpuTrainer* g) {
+    AttnParams a;
+    memset(&a, 0, sizeof(a));
+    a.B = (int)g->B; a.T = (int)g->T; a.H = (int)g->H; a.D = (int)g->D;
+    a.ldq = 3 * (int)g->D; a.ldo = (int)g->D;
+    a.scale = 1.0f / m_sqrtf((f32)g->hd);   /* attention.c:78 */
+    return a;
+}
+
+static void rope(GpuTrainer* g, hipDeviceptr_t qkv, i32 inverse) {
+    hipDeviceptr_t c = g->cos_t, s = g->sin_t;
+    i32 N = (i32)g->N, T = (i32)g->T, H = (i32)g->H, hd = (i32)g->hd, ld = 3 * (i32)g->D;
+    void* args[] = { &qkv, &c, &s, &N, &T, &H, &hd, &ld, &inverse };
+    hip_launch(g->k.rope_qk, cdiv_u64((u64)g->N * g->H * (g->hd / 2), 256), 1, 1, 256, 1, 1, 0, args);
+}
+
+/* ---------------- create / destroy ---------------- */
+
+GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,
+                              Node** params, u32 num_params, u32 batch_size, u32 seq_len) {
+    GpuTrainer g;
+    memset(&g, 0, sizeof(g));
+    g.V = model->vocab_size; g.D = model->d_model; g.H = model->num_heads; g.L = model->num_layers;
+    g.F = (u32)model->blocks[0].ffn.w_down->value.shape[0];
+    g.T = seq_len; g.B = batch_size; g.N = batch_size * seq_len;
+    g.hd = g.D / g.H;
+    g.eps = model->eps;
+    g.ldv = (g.V + 3u) & ~3u;
+    if (g.L > LM_MAX_LAYERS || num_params != 10u * g.L + 2u) fatal("parameter list does not match the model");
+    if (g.D % g.H != 0 || g.D % 4 != 0) fatal("d_model must be a multiple of 4 and of num_heads");
+    if (g.hd != 16 && g.hd != 32 && g.hd != 64) fatal("head_dim must be 16, 32 or 64");
+
+    g.hip = hip_init(alloc, ptx_path);
+    hip_set_current(&g.hip);
+    g.gemm = NULL;   /* created below, after g.hip has its final address in the caller */
+
+    g.num_params = num_params;
+    u64 off = 0;
+    for (u32 i = 0; i < num_params; i++) {
+        g.offsets[i] = off;
+        g.numels[i] = params[i]->value.numel;
+        off += params[i]->value.numel;
+    }
+    g.total_scalars = off;
+    g.params = dalloc(off);
+    g.grads = dalloc(off);
+    g.adam_m = dalloc(off);
+    g.adam_v = dalloc(off);
+    hip_memset_zero(g.adam_m, off * F4);
+    hip_memset_zero(g.adam_v, off * F4);
+    hip_memset_zero(g.grads, off * F4);
+
+    u64 N = g.N, D = g.D, F = g.F, BHT = (u64)g.B * g.H * g.T;
+    for (u32 l = 0; l < g.L; l++) {
+        GpuLayerActs* a = &g.layers[l];
+        a->x_in = dalloc(N * D);
+        a->n1 = dalloc(N * D);
+        a->r1 = dalloc(N);
+        a->qkv = dalloc(N * 3 * D);
+        a->att = dalloc(N * D);
+        a->lse = dalloc(BHT);
+        a->x2 = dalloc(N * D);
+        a->n2 = dalloc(N * D);
+        a->r2 = dalloc(N);
+        a->gu = dalloc(N * 2 * F);
+        a->h = dalloc(N * F);
+    }
+    g.x_final = dalloc(N * D);
+    g.nf = dalloc(N * D);
+    g.rf = dalloc(N);
+    g.logits = dalloc(N * (u64)g.ldv);
+    hip_memset_zero(g.logits, N * (u64)g.ldv * F4);
+
+    g.dres = dalloc(N * D);
+    g.dn = dalloc(N * D);
+    g.datt = dalloc(N * D);
+    g.dqkv = dalloc(N * 3 * D);
+    g.dh = dalloc(N * F);
+    g.dgu = dalloc(N * 2 * F);
+    g.dvec = dalloc(BHT);
+    u64 wide = 3 * D > 2 * F ? 3 * D : 2 * F;
+    u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;
+    u64 part_floats = part_rows * D;
+    if (((N + COLSUM_RPB - 1) / COLSUM_RPB) * wide > part_floats) part_floats = ((N + COLSUM_RPB - 1) / COLSUM_RPB) * wide;
+    g.part = dalloc(part_floats);
+
+    g.ids = hip_alloc(N * sizeof(u32));
+    g.targets = hip_alloc(N * sizeof(u32));
+    g.loss_rows = dalloc(N);
+    g.emb_order = hip_alloc(N * sizeof(u32));
+    g.emb_seg = hip_alloc((2 * N + 1) * sizeof(u32));
+    g.host_loss_rows = (f32*)allocator_alloc(alloc, N * F4);
+    g.host_emb = (u32*)allocator_alloc(alloc, (3 * N + 1 + (u64)g.V + 1) * sizeof(u32));
+    g.norm_partial = dalloc(GPU_TRAIN_NORM_BLOCKS);
+    g.host_norm_partial = (f32*)allocator_alloc(alloc, GPU_TRAIN_NORM_BLOCKS * F4);
+
+    /* RoPE tables, built on the host exactly as the CPU path builds them
+     * (gpu_train.c:239-247, model/rope.c) */
+    u64 cshape[2] = { g.T, g.hd / 2 };
+    Tensor cos_t = tensor_create(alloc, cshape, 2);
+    Tensor sin_t = tensor_create(alloc, cshape, 2);
+    rope_build_tables(&cos_t, &sin_t, g.T, g.hd, 10000.0f);
+    g.cos_t = dalloc(cos_t.numel);
+    g.sin_t = dalloc(sin_t.numel);
+    hip_h2d(g.cos_t, cos_t.data, cos_t.numel * F4);
+    hip_h2d(g.sin_t, sin_t.data, sin_t.numel * F4);
+
+    HipCtx* c = &g.hip;
+    g.k.fill_zero = hip_get_kernel(c, "k_fill_zero");
+    g.k.embed_fwd = hip_get_kernel(c, "k_embed_fwd");
+    g.k.embed_bwd = hip_get_kernel(c, "k_embed_bwd");
+    g.k.rmsnorm_fwd = hip_get_kernel(c, "k_rmsnorm_fwd");
+    g.k.rmsnorm_bwd = hip_get_kernel(c, "k_rmsnorm_bwd");
+    g.k.colsum_partial = hip_get_kernel(c, "k_colsum_partial");
+    g.k.colsum_final = hip_get_kernel(c, "k_colsum_final");
+    g.k.rope_qk = hip_get_kernel(c, "k_rope_qk");
+    g.k.swiglu_fwd = hip_get_kernel(c, "k_swiglu_fwd");
+    g.k.swiglu_bwd = hip_get_kernel(c, "k_swiglu_bwd");
+    g.k.cross_entropy = hip_get_kernel(c, "k_cross_entropy");
+    g.k.argmax_rows = hip_get_kernel(c, "k_argmax_rows");
+    g.k.sumsq_partial = hip_get_kernel(c, "k_sumsq_partial");
+    g.k.adam = hip_get_kernel(c, "k_adam");
+    char name[64];
+    snprintf(name, sizeof(name), "k_attn_fwd_hd%u", g.hd);
+    g.k.attn_fwd = hip_get_kernel(c, name);
+    snprintf(name, sizeof(name), "k_attn_bwd_dkv_hd%u", g.hd);
+    g.k.attn_bwd_dkv = hip_get_kernel(c, name);
+    snprintf(name, sizeof(name), "k_attn_bwd_dq_hd%u", g.hd);
+    g.k.attn_bwd_dq = hip_get_kernel(c, name);
+    g.k.attn_bwd_prep = hip_get_kernel(c, "k_attn_bwd_prep");
+
+    gpu_trainer_upload(&g, params, NULL_PTR);
+    hip_sync();
+    return g;
+}
+
+/* The GEMM engine keeps a pointer to the trainer's HipCtx, and the trainer
+ * is returned by value, so the engine is bound lazily on first use. */
+static void bind(GpuTrainer* g) {
+    hip_set_current(&g->hip);
+    if (!g->gemm) g->gemm = trlm_gemm_create(&g->hip);
+}
+
+void gpu_trainer_destroy(GpuTrainer* g) {
+    hip_set_current(&g->hip);
+    if (g->gemm) { trlm_gemm_destroy(g->gemm); g->gemm = NULL; }
+    hip_shutdown(&g->hip);   /* frees every buffer allocated for this trainer */
+}
+
+/* ---------------- CPU mirror <-> GPU (gpu_train.c:258-294) ---------------- */
+
+void gpu_trainer_upload(GpuTrainer* g, Node** params, const AdamOptimizer* opt) {
+    hip_set_current(&g->hip);
+    for (u32 i = 0; i < g->num_params; i++) {
+        hip_h2d(P_(g, i), params[i]->value.data, g->numels[i] * F4);
+        if (opt != NULL_PTR) {
+            hip_h2d(dptr(g->adam_m, g->offsets[i]), opt->m[i].data, g->numels[i] * F4);
+            hip_h2d(dptr(g->adam_v, g->offsets[i]), opt->v[i].data, g->numels[i] * F4);
+        }
+    }
+}
+
+void gpu_trainer_download(GpuTrainer* g, Node** params, AdamOptimizer* opt) {
+    hip_set_current(&g->hip);
+    for (u32 i = 0; i < g->num_params; i++) {
+        hip_d2h(params[i]->value.data, P_(g, i), g->numels[i] * F4);
+        if (opt != NULL_PTR) {
+            hip_d2h(opt->m[i].data, dptr(g->adam_m, g->offsets[i]), g->numels[i] * F4);
+            hip_d2h(opt->v[i].data, dptr(g->adam_v, g->offsets[i]), g->numels[i] * F4);
+        }
+    }
+}
+
+void gpu_trainer_download_grads(GpuTrainer* g, Node** params) {
+    hip_set_current(&g->hip);
+    for (u32 i = 0; i < g->num_params; i++) hip_d2h(params[i]->grad.data, G_(g, i), g->numels[i] * F4);
+}
+
+void gpu_trainer_upload_grads(GpuTrainer* g, Node** params) {
+    hip_set_current(&g->hip);
+    for (u32 i = 0; i < g->num_params; i++) hip_h2d(G_(g, i), params[i]->grad.data, g->numels[i] * F4);
+}
+
+/* Window of sequence w: pcg_seed(seed_base*1000003 + w, 99 + w), start
+ * uniform in [0, num_tokens - T - 1)  (gpu_train.c:296-307). */
+void gpu_trainer_sample_batch(const u32* tokens, u64 num_tokens, u32 seq_len, u32 batch_size,
+                              u64 seed_base, u32* ids_out, u32* targets_out) {
+    i64 max_start = (i64)(num_tokens - seq_len - 1);
+    for (u32 w = 0; w < batch_size; w++) {
+        PCGState rng = pcg_seed(seed_base * 1000003ull + w, 99ull + w);
+        i64 start = pcg_range_i64(&rng, 0, max_start);
+        for (u32 t = 0; t < seq_len; t++) {
+            ids_out[(u64)w * seq_len + t] = tokens[start + t];
+            targets_out[(u64)w * seq_len + t] = tokens[start + t + 1];
+        }
+    }
+}
+
+/* ---------------- forward / backward ---------------- */
+
+/* Stable counting sort of the rows by token id: rows of one token form a
+ * segment, listed in ascending row order (the order in which the reference
+ * adds them, embedding.c:10-14). */
+static void embed_segments(GpuTrainer* g, const u32* ids) {
+    u32 N = g->N, V = g->V;
+    u32* order = g->host_emb;
+    u32* seg = order + N;            /* seg_start[nseg+1] then seg_tok[nseg] */
+    u32* count = seg + 2 * N + 1;    /* [V+1] */
+    memset(count, 0, ((u64)V + 1) * sizeof(u32));
+    for (u32 n = 0; n < N; n++) {
+        if (ids[n] >= V) fatal("token id outside the vocabulary");
+        count[ids[n] + 1]++;
+    }
+    u32 nseg = 0;
+    for (u32 v = 0; v < V; v++) if (count[v + 1]) nseg++;
+    u32* seg_start = seg;
+    u32* seg_tok = seg + nseg + 1;
+    u32 s = 0;
+    for (u32 v = 0; v < V; v++) {
+        u32 c = count[v + 1];
+        count[v + 1] = count[v] + c;   /* count[v] = first slot of token v */
+        if (c) { seg_start[s] = count[v]; seg_tok[s] = v; s++; }
+    }
+    seg_start[nseg] = N;
+    for (u32 n = 0; n < N; n++) order[count[ids[n]]++] = n;
+    g->emb_nseg = nseg;
+    hip_h2d(g->emb_order, order, (u64)N * sizeof(u32));
+    hip_h2d(g->emb_seg, seg, (2ull * nseg + 1) * sizeof(u32));
+}
+
+/* Embedding, L blocks, final norm, tied head (model/gpu_train.c:312-378). */
+static void check_ids(const GpuTrainer* g, const u32* ids, const char* what) {
+    for (u32 n = 0; n < g->N; n++)
+        if (ids[n] >= g->V) {
+            fprintf(stderr, "[HIP ERROR] gpu_train: %s[%u] = %u is outside the vocabulary (%u)\n", what, n, ids[n],
+                    g->V);
+            fflush(stderr);
+            _exit(1);
+        }
+}
+
+static void forward_to_logits(GpuTrainer* g, const u32* ids) {
+    i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F, V = (i32)g->V, ldv = (i32)g->ldv;
+    check_ids(g, ids, "ids");
+    hip_h2d(g->ids, ids, (u64)N * sizeof(u32));
+    {
+        hipDeviceptr_t E = P_(g, 0), idp = g->ids, x0 = g->layers[0].x_in;
+        void* args[] = { &E, &idp, &x0, &N, &D };
+        u64 work = (D % 4 == 0) ? (u64)N * D / 4 : (u64)N * D;
+        hip_launch(g->k.embed_fwd, cdiv_u64(work, 256), 1, 1, 256, 1, 1, 0, args);
+    }
+    AttnParams ap = attn_params(g);
+    for (u32 l = 0; l < g->L; l++) {
+        GpuLayerActs* a = &g->layers[l];
+        hipDeviceptr_t x_out = (l + 1 < g->L) ? g->layers[l + 1].x_in : g->x_final;
+        rmsnorm_fwd(g, a->x_in, P_(g, pidx(l, PK_ATTN_NORM)), a->n1, a->r1);
+        gemm1(g, GEMM_NN, a->n1, P_(g, pidx(l, PK_WQKV)), a->qkv, N, 3 * D, D, D, 3 * D, 3 * D, 0.0f,
+              P_(g, pidx(l, PK_BQKV)), NULL);
+        rope(g, a->qkv, 0);
+        ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
+        {
+            void* args[] = { &ap };
+            hip_launch(g->k.attn_fwd, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
+        }
+        /* x2 = x_in + (att @ Wo + bo) */
+        gemm1(g, GEMM_NN, a->att, P_(g, pidx(l, PK_WO)), a->x2, N, D, D, D, D, D, 0.0f, P_(g, pidx(l, PK_BO)),
+              a->x_in);
+        rmsnorm_fwd(g, a->x2, P_(g, pidx(l, PK_FFN_NORM)), a->n2, a->r2);
+        gemm1(g, GEMM_NN, a->n2, P_(g, pidx(l, PK_WGU)), a->gu, N, 2 * F, D, D, 2 * F, 2 * F, 0.0f,
+              P_(g, pidx(l, PK_BGU)), NULL);
+        {
+            hipDeviceptr_t gu = a->gu, h = a->h;
+            void* args[] = { &gu, &h, &N, &F };
+            hip_launch(g->k.swiglu_fwd, cdiv_u64((u64)N * F, 256), 1, 1, 256, 1, 1, 0, args);
+        }
+        /* x_out = x2 + (h @ Wd + bd) */
+        gemm1(g, GEMM_NN, a->h, P_(g, pidx(l, PK_WDOWN)), x_out, N, D, F, F, D, D, 0.0f, P_(g, pidx(l, PK_BDOWN)),
+              a->x2);
+    }
+    rmsnorm_fwd(g, g->x_final, P_(g, pidx(g->L, 0)), g->nf, g->rf);
+    /* logits = nf @ E^T  (tied head, NT with B = E [V, D]) */
+    gemm1(g, GEMM_NT, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 0.0f, NULL, NULL);
+}
+
+static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
+    check_ids(g, targets, "targets");
+    hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
+    hipDeviceptr_t lg = g->logits, tg = g->targets, lr = g->loss_rows;
+    i32 ld = (i32)g->ldv, V = (i32)g->V;
+    f32 grad_scale = 1.0f / (f32)g->N;
+    void* args[] = { &lg, &ld, &tg, &lr, &V, &grad_scale, &write_grad };
+    hip_launch(g->k.cross_entropy, g->N, 1, 1, 256, 1, 1, 0, args);
+}
+
+/* Gradients of every parameter from dlogits left in g->logits
+ * (model/gpu_train.c:390-474).  Weight-gradient GEMMs write (beta = 0):
+ * each weight receives exactly one contribution per step. */
+static void backward_pass(GpuTrainer* g) {
+    i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F, V = (i32)g->V, ldv = (i32)g->ldv;
+    u32 p_final = pidx(g->L, 0);
+
+    /* tied head: dE = dlogits^T @ nf ; dnf = dlogits @ E */
+    gemm1(g, GEMM_TN, g->logits, g->nf, G_(g, 0), V, D, N, ldv, D, D, 0.0f, NULL, NULL);
+    gemm1(g, GEMM_NN, g->logits, P_(g, 0), g->dn, N, D, V, ldv, D, D, 0.0f, NULL, NULL);
+    fill_zero(g, g->dres, (u64)N * D);
+    rmsnorm_bwd(g, g->x_final, P_(g, p_final), g->rf, g->dn, g->dres, G_(g, p_final));
+
+    AttnParams ap = attn_params(g);
+    for (i32 l = (i32)g->L - 1; l >= 0; l--) {
+        GpuLayerActs* a = &g->layers[l];
+        u32 ul = (u32)l;
+        /* FFN: x3 = x2 + (h @ Wd + bd); dres = dx3 */
+        gemm1(g, GEMM_TN, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), F, D, N, F, D, D, 0.0f, NULL, NULL);
+        colsum(g, g->dres, G_(g, pidx(ul, PK_BDOWN)), N, D);
+        gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WDOWN)), g->dh, N, F, D, D, D, F, 0.0f, NULL, NULL);
+        {
+            hipDeviceptr_t gu = a->gu, dh = g->dh, dgu = g->dgu;
+            void* args[] = { &gu, &dh, &dgu, &N, &F };
+            hip_launch(g->k.swiglu_bwd, cdiv_u64((u64)N * F, 256), 1, 1, 256, 1, 1, 0, args);
+        }
+        gemm1(g, GEMM_TN, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), D, 2 * F, N, D, 2 * F, 2 * F, 0.0f, NULL, NULL);
+        colsum(g, g->dgu, G_(g, pidx(ul, PK_BGU)), N, 2 * F);
+        gemm1(g, GEMM_NT, g->dgu, P_(g, pidx(ul, PK_WGU)), g->dn, N, D, 2 * F, 2 * F, 2 * F, D, 0.0f, NULL, NULL);
+        rmsnorm_bwd(g, a->x2, P_(g, pidx(ul, PK_FFN_NORM)), a->r2, g->dn, g->dres, G_(g, pidx(ul, PK_FFN_NORM)));
+        /* attention: x2 = x + (att @ Wo + bo); dres = dx2 */
+        gemm1(g, GEMM_TN, a->att, g->dres, G_(g, pidx(ul, PK_WO)), D, D, N, D, D, D, 0.0f, NULL, NULL);
+        colsum(g, g->dres, G_(g, pidx(ul, PK_BO)), N, D);
+        gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
+        ap.qkv = (const float*)a->qkv; ap.O = (const float*)a->att; ap.dO = (const float*)g->datt;
+        ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
+        {
+            void* args[] = { &ap };
+            hip_launch(g->k.attn_bwd_prep, cdiv_u64((u64)g->N * g->H, 256), 1, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dkv, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dq, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
+        }
+        rope(g, g->dqkv, 1);
+        gemm1(g, GEMM_TN, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), D, 3 * D, N, D, 3 * D, 3 * D, 0.0f, NULL,
+              NULL);
+        colsum(g, g->dqkv, G_(g, pidx(ul, PK_BQKV)), N, 3 * D);
+        gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,
+              NULL);
+        rmsnorm_bwd(g, a->x_in, P_(g, pidx(ul, PK_ATTN_NORM)), a->r1, g->dn, g->dres,
+                    G_(g, pidx(ul, PK_ATTN_NORM)));
+    }
+    /* embedding: dE[tok] += rows of dres, per token in ascending row order */
+    {
+        hipDeviceptr_t dx = g->dres, order = g->emb_order, seg = g->emb_seg, dE = G_(g, 0);
+        hipDeviceptr_t seg_tok = dptr(seg, g->emb_nseg + 1);
+        i32 nseg = (i32)g->emb_nseg;
+        void* args[] = { &dx, &order, &seg, &seg_tok, &nseg, &dE, &D };
+        hip_launch(g->k.embed_bwd, g->emb_nseg, cdiv_u64((u64)D, 256), 1, 256, 1, 1, 0, args);
+    }
+}
+
+/* Per-sequence mean then mean over sequences (gpu_train.c:476-487). */
+static f32 mean_loss(GpuTrainer* g) {
+    hip_d2h(g->host_loss_rows, g->loss_rows, (u64)g->N * F4);
+    f32 loss_sum = 0.0f;
+    for (u32 b = 0; b < g->B; b++) {
+        f32 s = 0.0f;
+        for (u32 t = 0; t < g->T; t++) s += g->host_loss_rows[(u64)b * g->T + t];
+        loss_sum += s / (f32)g->T;
+    }
+    return loss_sum / (f32)g->B;
+}
+
+f32 gpu_trainer_forward_backward(GpuTrainer* g, const u32* ids, const u32* targets) {
+    bind(g);
+    embed_segments(g, ids);
+    forward_to_logits(g, ids);
+    cross_entropy(g, targets, 1);
+    backward_pass(g);
+    return mean_loss(g);
+}
+
+f32 gpu_trainer_eval_loss(GpuTrainer* g, const u32* ids, const u32* targets) {
+    bind(g);
+    forward_to_logits(g, ids);
+    cross_entropy(g, targets, 1);
+    return mean_loss(g);
+}
+
+/* Deterministic L2 norm: fixed grid of partial sums, f64 host sum in order
+ * (gpu_train.c:502-512). */
+f64 gpu_trainer_grad_norm(GpuTrainer* g) {
+    bind(g);
+    hipDeviceptr_t x = g->grads, part = g->norm_partial;
+    long long n = (long long)g->total_scalars;
+    void* args[] = { &x, &n, &part };
+    hip_launch(g->k.sumsq_partial, GPU_TRAIN_NORM_BLOCKS, 1, 1, 256, 1, 1, 0, args);
+    hip_d2h(g->host_norm_partial, g->norm_partial, GPU_TRAIN_NORM_BLOCKS * F4);
+    f64 ss = 0.0;
+    for (u32 i = 0; i < GPU_TRAIN_NORM_BLOCKS; i++) ss += (f64)g->host_norm_partial[i];
+    return m_sqrt(ss);
+}
+
+static void adam_launch(GpuTrainer* g, AdamOptimizer* opt, f32 grad_scale, f32 weight_decay) {
+    bind(g);
+    opt->t++;
+    f32 bc1 = 1.0f - m_powf(opt->beta1, (f32)opt->t);
+    f32 bc2 = 1.0f - m_powf(opt->beta2, (f32)opt->t);
+    hipDeviceptr_t p = g->params, gr = g->grads, m = g->adam_m, v = g->adam_v;
+    long long n = (long long)g->total_scalars;
+    f32 lr = opt->lr, b1 = opt->beta1, b2 = opt->beta2, eps = opt->eps;
+    f32 lrwd = lr * weight_decay;
+    void* args[] = { &p, &gr, &m, &v, &n, &lr, &b1, &b2, &eps, &bc1, &bc2, &grad_scale, &lrwd };
+    u32 blocks = cdiv_u64((u64)(n / 4) > 0 ? (u64)(n / 4) : 1, 256);
+    hip_launch(g->k.adam, blocks, 1, 1, 256, 1, 1, 0, args);
+    hip_sync();
+}
+
+void gpu_trainer_adam_step(GpuTrainer* g, AdamOptimizer* opt) { gpu_trainer_adam_step_scaled(g, opt, 1.0f); }
+
+void gpu_trainer_adam_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 grad_scale) {
+    adam_launch(g, opt, grad_scale, 0.0f);
+}
+
+/* ---------------- additive entry points (trlm_ext.h) ---------------- */
+
+static void logits_to_host(GpuTrainer* g, f32* host) {
+    hipError_t r = hipMemcpy2DAsync(host, (size_t)g->V * F4, g->logits, (size_t)g->ldv * F4, (size_t)g->V * F4,
+                                    g->N, hipMemcpyDeviceToHost, g->hip.stream);
+    if (r != hipSuccess) fatal("logits copy failed");
+    hip_sync();
+}
+
+void gpu_trainer_forward_logits(GpuTrainer* g, const u32* ids, f32* host_logits) {
+    bind(g);
+    forward_to_logits(g, ids);
+    if (host_logits) logits_to_host(g, host_logits);
+    else hip_sync();
+}
+
+f32 gpu_trainer_forward_loss_logits(GpuTrainer* g, const u32* ids, const u32* targets, f32* host_logits) {
+    bind(g);
+    forward_to_logits(g, ids);
+    cross_entropy(g, targets, 0);
+    f32 loss = mean_loss(g);
+    if (host_logits) logits_to_host(g, host_logits);
+    return loss;
+}
+
+void gpu_trainer_greedy_argmax(GpuTrainer* g, u32* host_ids_out) {
+    bind(g);
+    hipDeviceptr_t lg = g->logits, out = g->emb_order;   /* [N] u32 scratch */
+    i32 ld = (i32)g->ldv, V = (i32)g->V;
+    void* args[] = { &lg, &ld, &V, &out };
+    hip_launch(g->k.argmax_rows, g->N, 1, 1, 256, 1, 1, 0, args);
+    hip_d2h(host_ids_out, out, (u64)g->N * sizeof(u32));
+}
+
+void gpu_trainer_adamw_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay, f32 grad_scale) {
+    adam_launch(g, opt, grad_scale, weight_decay);
+}

@@ -1,0 +1,207 @@
+/* hip_backend.c -- HIP module-API backend (see include/hip_backend.h).
+ *
+ * Role of cuda/cuda_backend.c (cuda_backend.c:15-161): fatal error check,
+ * kernel image load, allocation, synchronous copies and launch helpers.
+ */
+#include "hip_backend.h"
+
+#include <pthread.h>
+#include <stdio.h>
+#include <stdlib.h>
+#include <string.h>
+#include <unistd.h>
+
+struct HipAllocList {
+    pthread_mutex_t lock;
+    void** ptrs;
+    u64 count;
+    u64 cap;
+};
+
+static _Thread_local HipCtx* tls_ctx = NULL;
+
+static void fatal_exit(void) {
+    fflush(stdout);
+    fflush(stderr);
+    _exit(1);
+}
+
+/* Same convention as the reference (cuda_backend.c:23-34): name what failed,
+ * the error's name and description, and end the process. */
+static void check(hipError_t r, const char* what) {
+    if (r != hipSuccess) {
+        fprintf(stderr, "[HIP ERROR] %s -> %s: %s\n", what, hipGetErrorName(r), hipGetErrorString(r));
+        fatal_exit();
+    }
+}
+
+static void* read_image(Allocator* scratch, const char* path, u64* out_size) {
+    FILE* f = fopen(path, "rb");
+    if (!f) {
+        fprintf(stderr, "[HIP ERROR] cannot open kernel image: %s\n", path);
+        fatal_exit();
+    }
+    fseek(f, 0, SEEK_END);
+    long size = ftell(f);
+    fseek(f, 0, SEEK_SET);
+    u8* buf = scratch ? (u8*)allocator_alloc(scratch, (u64)size + 1) : (u8*)malloc((size_t)size + 1);
+    size_t got = fread(buf, 1, (size_t)size, f);
+    fclose(f);
+    if (got != (size_t)size) {
+        fprintf(stderr, "[HIP ERROR] short read of kernel image: %s\n", path);
+        fatal_exit();
+    }
+    buf[size] = 0;
+    *out_size = (u64)size;
+    return buf;
+}
+
+HipCtx hip_init_on_device(Allocator* scratch, const char* image_path, i32 device_index) {
+    HipCtx c;
+    memset(&c, 0, sizeof(c));
+    i32 count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    if (count < 1) {
+        fprintf(stderr, "[HIP ERROR] no HIP device found\n");
+        fatal_exit();
+    }
+    if (device_index < 0 || device_index >= count) {
+        fprintf(stderr, "[HIP ERROR] device index %d exceeds the %d visible devices\n", device_index, count);
+        fatal_exit();
+    }
+    c.device = device_index;
+    check(hipSetDevice(device_index), "hipSetDevice");
+    u64 size;
+    void* image = read_image(scratch, image_path, &size);
+    check(hipModuleLoadData(&c.module, image), "hipModuleLoadData");
+    if (!scratch) free(image);
+    check(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+    c.allocs = (HipAllocList*)calloc(1, sizeof(HipAllocList));
+    pthread_mutex_init(&c.allocs->lock, NULL);
+    return c;
+}
+
+HipCtx hip_init(Allocator* scratch, const char* image_path) {
+    return hip_init_on_device(scratch, image_path, 0);
+}
+
+i32 hip_device_count(void) {
+    i32 count = 0;
+    check(hipGetDeviceCount(&count), "hipGetDeviceCount");
+    return count;
+}
+
+void hip_shutdown(HipCtx* c) {
+    if (!c->allocs) return;
+    check(hipSetDevice(c->device), "hipSetDevice");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    for (u64 i = 0; i < c->allocs->count; i++)
+        if (c->allocs->ptrs[i]) check(hipFree(c->allocs->ptrs[i]), "hipFree");
+    free(c->allocs->ptrs);
+    pthread_mutex_destroy(&c->allocs->lock);
+    free(c->allocs);
+    c->allocs = NULL;
+    check(hipStreamDestroy(c->stream), "hipStreamDestroy");
+    check(hipModuleUnload(c->module), "hipModuleUnload");
+    if (tls_ctx == c) tls_ctx = NULL;
+}
+
+void hip_set_current(HipCtx* c) {
+    check(hipSetDevice(c->device), "hipSetDevice");
+    tls_ctx = c;
+}
+
+static HipCtx* current(const char* what) {
+    if (!tls_ctx) {
+        fprintf(stderr, "[HIP ERROR] %s: no context is current on this thread\n", what);
+        fatal_exit();
+    }
+    return tls_ctx;
+}
+
+hipStream_t hip_current_stream(void) { return current("hip_current_stream")->stream; }
+
+hipFunction_t hip_get_kernel(HipCtx* c, const char* name) {
+    hipFunction_t f;
+    hipError_t r = hipModuleGetFunction(&f, c->module, name);
+    if (r != hipSuccess) {
+        fprintf(stderr, "[HIP ERROR] hipModuleGetFunction(%s) -> %s: %s\n", name, hipGetErrorName(r),
+                hipGetErrorString(r));
+        fatal_exit();
+    }
+    return f;
+}
+
+hipDeviceptr_t hip_alloc(u64 bytes) {
+    HipCtx* c = current("hip_alloc");
+    void* p = NULL;
+    check(hipMalloc(&p, bytes ? bytes : 4), "hipMalloc");
+    HipAllocList* l = c->allocs;
+    pthread_mutex_lock(&l->lock);
+    if (l->count == l->cap) {
+        l->cap = l->cap ? l->cap * 2 : 256;
+        l->ptrs = (void**)realloc(l->ptrs, l->cap * sizeof(void*));
+    }
+    l->ptrs[l->count++] = p;
+    pthread_mutex_unlock(&l->lock);
+    return p;
+}
+
+void hip_free(hipDeviceptr_t p) {
+    HipCtx* c = current("hip_free");
+    HipAllocList* l = c->allocs;
+    pthread_mutex_lock(&l->lock);
+    for (u64 i = l->count; i-- > 0;) {
+        if (l->ptrs[i] == p) { l->ptrs[i] = l->ptrs[--l->count]; break; }
+    }
+    pthread_mutex_unlock(&l->lock);
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    check(hipFree(p), "hipFree");
+}
+
+void hip_h2d(hipDeviceptr_t dst, const void* src, u64 bytes) {
+    HipCtx* c = current("hip_h2d");
+    check(hipMemcpyHtoDAsync(dst, (void*)src, bytes, c->stream), "hipMemcpyHtoDAsync");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+void hip_d2h(void* dst, hipDeviceptr_t src, u64 bytes) {
+    HipCtx* c = current("hip_d2h");
+    check(hipMemcpyDtoHAsync(dst, src, bytes, c->stream), "hipMemcpyDtoHAsync");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}
+
+void hip_launch(hipFunction_t f, u32 gx, u32 gy, u32 gz, u32 bx, u32 by, u32 bz, u32 shared_bytes,
+                void** params) {
+    HipCtx* c = current("hip_launch");
+    if (gx == 0 || gy == 0 || gz == 0) return;
+    check(hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, shared_bytes, c->stream, params, NULL),
+          "hipModuleLaunchKernel");
+}
+
+#define BLOCK_1D 256u
+
+void hip_launch_1d(hipFunction_t f, u32 n, void** params) {
+    hip_launch(f, (n + BLOCK_1D - 1) / BLOCK_1D, 1, 1, BLOCK_1D, 1, 1, 0, params);
+}
+
+void hip_launch_1d_shared(hipFunction_t f, u32 n, u32 block_size, u32 shared_bytes, void** params) {
+    hip_launch(f, (n + block_size - 1) / block_size, 1, 1, block_size, 1, 1, shared_bytes, params);
+}
+
+#define BLOCK_2D 16u
+
+void hip_launch_2d(hipFunction_t f, u32 rows, u32 cols, void** params) {
+    hip_launch(f, (cols + BLOCK_2D - 1) / BLOCK_2D, (rows + BLOCK_2D - 1) / BLOCK_2D, 1, BLOCK_2D, BLOCK_2D, 1,
+               0, params);
+}
+
+void hip_memset_zero(hipDeviceptr_t p, u64 bytes) {
+    HipCtx* c = current("hip_memset_zero");
+    check(hipMemsetD8Async(p, 0, bytes, c->stream), "hipMemsetD8Async");
+}
+
+void hip_sync(void) {
+    HipCtx* c = current("hip_sync");
+    check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+}

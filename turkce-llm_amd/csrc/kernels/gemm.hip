@@ -1,0 +1,291 @@
+// gemm.hip -- fp32 GEMMs on CDNA4 FP32 matrix cores (v_mfma_f32_32x32x2f32).
+//
+// C[M,N] = alpha * op(A) @ op(B) (+ beta*C) (+ bias[n]) (+ resid[m,n])
+//   TA=0: A stored [M,K] (lda)     TA=1: A stored [K,M] -> op(A) = A^T
+//   TB=0: B stored [K,N] (ldb)     TB=1: B stored [N,K] -> op(B) = B^T
+// Batched through blockIdx.z (element strides sA/sB/sC), with an optional
+// deterministic split-K: split s of a batch entry covers K-range
+// [s*kchunk, (s+1)*kchunk) and writes its raw partial to C + s*sW; the
+// partials are then summed in split order by k_gemm_splitk_reduce.
+// Same contract as the reference's k_gemm_nn/nt/tn and k_bf16_gemm_nn_bias
+// (train_kernels.cu:97-193,226-329), computed in fp32 only.
+//
+// Design (MI355X):
+//  - 256-thread workgroups = 4 wave64 in a 2x2 grid; each wave owns a
+//    (BM/2)x(BN/2) block of 32x32 MFMA accumulators.
+//  - Operands are staged through double-buffered LDS, one barrier per
+//    BK=16 step; the next global tile is prefetched into registers while the
+//    current one feeds the matrix cores.
+//  - A K-contiguous operand is kept K-contiguous in LDS and read with one
+//    128-bit LDS read per 4 MFMA steps: lane l feeds k = kk+4*(l/32)+s at
+//    step s, a permutation of k that both operands share.  An MN-contiguous
+//    operand is kept MN-contiguous and read 32 consecutive floats per
+//    half-wave (conflict-free).
+//  - Tiles are visited XCD-aware: consecutive workgroups land on different
+//    XCDs, so the tile index is remapped so that each XCD works on a
+//    contiguous, M-grouped range of tiles and reuses operands in its own L2.
+#include "common.h"
+
+struct GemmParams {
+    const float* A;
+    const float* B;
+    float* C;
+    const float* bias;
+    const float* resid;
+    long long sA, sB, sC, sW;
+    int M, N, K;
+    int lda, ldb, ldc, ldr;
+    int splits, kchunk;
+    float alpha, beta;
+    int tiles_m, tiles_n;
+};
+
+#define GBK 16
+
+__device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
+    const int num = p.tiles_m * p.tiles_n;
+    int bid = blockIdx.x;
+    // XCD-aware remap: hardware hands workgroup i to XCD (i % 8).
+    const int per = num >> 3;
+    int tile = bid;
+    if (bid < (per << 3)) tile = (bid & 7) * per + (bid >> 3);
+    // Group 8 M-tiles so tiles that run together share A and B panels.
+    const int GROUP = 8;
+    int group_size = GROUP * p.tiles_n;
+    int g = tile / group_size;
+    int first_m = g * GROUP;
+    int gm = p.tiles_m - first_m;
+    if (gm > GROUP) gm = GROUP;
+    int in = tile - g * group_size;
+    tm = first_m + in % gm;
+    tn = in / gm;
+}
+
+template <int R, bool KMAJOR>
+struct TileLds {
+    // KMAJOR: [R][GBK+4] (k contiguous); else [GBK][R] (m/n contiguous)
+    static constexpr int SIZE = KMAJOR ? R * (GBK + 4) : GBK * R;
+};
+
+// Load one operand tile (R rows of m/n, GBK of k) from global memory into
+// registers.  KMAJOR: element (r, k) at base[r*ld + k]; else base[k*ld + r].
+template <int R, bool KMAJOR, bool ALIGNED>
+__device__ __forceinline__ void load_tile(const float* __restrict__ base, int ld, int r0, int rlim, int k0,
+                                          int klim, f32x4* regs) {
+    constexpr int NL = R * GBK / 4 / 256;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        int idx = t + i * 256;
+        int r, k;
+        if (KMAJOR) { r = idx >> 2; k = (idx & 3) * 4; }
+        else { k = idx / (R / 4); r = (idx % (R / 4)) * 4; }
+        int gr = r0 + r, gk = k0 + k;
+        f32x4 v = {0.f, 0.f, 0.f, 0.f};
+        if (KMAJOR) {
+            if (gr < rlim) {
+                const float* src = base + (long long)gr * ld + gk;
+                if (ALIGNED && gk + 3 < klim) {
+                    v = *(const f32x4*)src;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = (gk + e < klim) ? src[e] : 0.f;
+                }
+            }
+        } else {
+            if (gk < klim) {
+                const float* src = base + (long long)gk * ld + gr;
+                if (ALIGNED && gr + 3 < rlim) {
+                    v = *(const f32x4*)src;
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; e++) v[e] = (gr + e < rlim) ? src[e] : 0.f;
+                }
+            }
+        }
+        regs[i] = v;
+    }
+}
+
+template <int R, bool KMAJOR>
+__device__ __forceinline__ void store_tile(float* lds, const f32x4* regs) {
+    constexpr int NL = R * GBK / 4 / 256;
+    const int t = threadIdx.x;
+#pragma unroll
+    for (int i = 0; i < NL; i++) {
+        int idx = t + i * 256;
+        if (KMAJOR) {
+            int r = idx >> 2, k = (idx & 3) * 4;
+            *(f32x4*)(lds + r * (GBK + 4) + k) = regs[i];
+        } else {
+            int k = idx / (R / 4), r = (idx % (R / 4)) * 4;
+            *(f32x4*)(lds + k * R + r) = regs[i];
+        }
+    }
+}
+
+// Operand values of one 32-row MFMA block for the 4 steps of an 8-k chunk.
+template <int R, bool KMAJOR>
+__device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, int lane) {
+    const int row = rb + (lane & 31);
+    const int kq = kk + 4 * (lane >> 5);
+    if (KMAJOR) {
+        return *(const f32x4*)(lds + row * (GBK + 4) + kq);
+    } else {
+        f32x4 v;
+#pragma unroll
+        for (int s = 0; s < 4; s++) v[s] = lds[(kq + s) * R + row];
+        return v;
+    }
+}
+
+template <int TA, int TB, int BM, int BN, bool ALIGNED>
+__device__ __forceinline__ void gemm_body(const GemmParams& p) {
+    constexpr bool AK = (TA == 0);   // A K-contiguous
+    constexpr bool BK_ = (TB == 1);  // B K-contiguous
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int ASZ = TileLds<BM, AK>::SIZE, BSZ = TileLds<BN, BK_>::SIZE;
+    constexpr int NLA = BM * GBK / 4 / 256, NLB = BN * GBK / 4 / 256;
+    __shared__ __attribute__((aligned(16))) float lds[2 * (ASZ + BSZ)];
+
+    int tm, tn;
+    gemm_tile_coords(p, tm, tn);
+    const int z = blockIdx.z;
+    const int batch = z / p.splits, split = z - batch * p.splits;
+    const float* A = p.A + batch * p.sA;
+    const float* B = p.B + batch * p.sB;
+    float* C = p.C + batch * p.sC + split * p.sW;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kb = split * p.kchunk;
+    int ke = kb + p.kchunk;
+    if (ke > p.K) ke = p.K;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    f32x4 ra[NLA > 0 ? NLA : 1], rb[NLB > 0 ? NLB : 1];
+    auto gload = [&](int k0) {
+        if (AK) load_tile<BM, true, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+        else load_tile<BM, false, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+        if (BK_) load_tile<BN, true, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+        else load_tile<BN, false, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+    };
+    auto lstore = [&](int buf) {
+        store_tile<BM, AK>(lds + buf * (ASZ + BSZ), ra);
+        store_tile<BN, BK_>(lds + buf * (ASZ + BSZ) + ASZ, rb);
+    };
+
+    const int nk = (ke - kb + GBK - 1) / GBK;
+    if (nk > 0) {
+        gload(kb);
+        lstore(0);
+    }
+    __syncthreads();
+    for (int kt = 0; kt < nk; kt++) {
+        const int cur = kt & 1;
+        if (kt + 1 < nk) gload(kb + (kt + 1) * GBK);
+        const float* la = lds + cur * (ASZ + BSZ);
+        const float* lb = la + ASZ;
+#pragma unroll
+        for (int kk = 0; kk < GBK; kk += 8) {
+            f32x4 fa[FM], fb[FN];
+#pragma unroll
+            for (int i = 0; i < FM; i++) fa[i] = fetch_frag<BM, AK>(la, wm0 + i * 32, kk, lane);
+#pragma unroll
+            for (int j = 0; j < FN; j++) fb[j] = fetch_frag<BN, BK_>(lb, wn0 + j * 32, kk, lane);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+        }
+        if (kt + 1 < nk) lstore(cur ^ 1);
+        __syncthreads();
+    }
+
+    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.
+    const int half = lane >> 5, col_l = lane & 31;
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++) {
+            const int col = n0 + wn0 + j * 32 + col_l;
+            if (col >= p.N) continue;
+            const float bv = p.bias ? p.bias[col] : 0.f;
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (row < p.M) {
+                    float v = p.alpha * acc[i][j][r];
+                    float* dst = C + (long long)row * p.ldc + col;
+                    if (p.beta != 0.f) v = v + p.beta * *dst;
+                    if (p.bias) v = v + bv;
+                    if (p.resid) v = p.resid[(long long)row * p.ldr + col] + v;
+                    *dst = v;
+                }
+            }
+        }
+}
+
+#define GEMM_KERNEL(NAME, TA, TB, BM, BN, AL)                                           \
+    extern "C" __global__ void __launch_bounds__(256) NAME(GemmParams p) {             \
+        gemm_body<TA, TB, BM, BN, AL>(p);                                              \
+    }
+
+// name: k_gemm_<layout>_<BM>x<BN>[_u]  (_u = unaligned operands, scalar loads)
+GEMM_KERNEL(k_gemm_nn_128x128, 0, 0, 128, 128, true)
+GEMM_KERNEL(k_gemm_nn_64x128, 0, 0, 64, 128, true)
+GEMM_KERNEL(k_gemm_nn_64x64, 0, 0, 64, 64, true)
+GEMM_KERNEL(k_gemm_nt_128x128, 0, 1, 128, 128, true)
+GEMM_KERNEL(k_gemm_nt_64x128, 0, 1, 64, 128, true)
+GEMM_KERNEL(k_gemm_nt_64x64, 0, 1, 64, 64, true)
+GEMM_KERNEL(k_gemm_tn_128x128, 1, 0, 128, 128, true)
+GEMM_KERNEL(k_gemm_tn_64x128, 1, 0, 64, 128, true)
+GEMM_KERNEL(k_gemm_tn_64x64, 1, 0, 64, 64, true)
+GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, false)
+GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, false)
+GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, false)
+GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, false)
+
+// out[m,n] = alpha * sum_s W[s][m,n] (+ beta*out) (+ bias[n]); out = resid + v.
+// Partials are summed in split order, so the result is reproducible.
+extern "C" __global__ void __launch_bounds__(256)
+k_gemm_splitk_reduce(const float* __restrict__ W, int splits, long long sW, float* __restrict__ C, int M, int N,
+                     int ldc, float alpha, float beta, const float* __restrict__ bias,
+                     const float* __restrict__ resid, int ldr) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)M * N) return;
+    int m = (int)(i / N), n = (int)(i - (long long)m * N);
+    float s = W[i];
+    for (int k = 1; k < splits; k++) s += W[k * sW + i];
+    float v = alpha * s;
+    float* dst = C + (long long)m * ldc + n;
+    if (beta != 0.f) v = v + beta * *dst;
+    if (bias) v = v + bias[n];
+    if (resid) v = resid[(long long)m * ldr + n] + v;
+    *dst = v;
+}
+
+// Writes the raw accumulator of one MFMA whose A and B operands are the
+// lane's own values, so a host test can confirm the operand/result lane
+// layout the GEMMs assume.  out: [64 lanes][16 registers].
+extern "C" __global__ void k_mfma_layout_probe(const float* a, const float* b, float* out) {
+    int l = threadIdx.x;
+    f32x16 acc;
+#pragma unroll
+    for (int r = 0; r < 16; r++) acc[r] = 0.f;
+    acc = __builtin_amdgcn_mfma_f32_32x32x2f32(a[l], b[l], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 16; r++) out[l * 16 + r] = acc[r];
+}

@@ -1,0 +1,335 @@
+// rowops.hip -- HBM-bound row and elementwise kernels of the training step.
+//
+// Counterparts of the reference's non-GEMM kernels (train_kernels.cu:498-800),
+// laid out for wave64: one wavefront per row for the D=384 row reductions,
+// float4 accesses where rows are 16-byte aligned, and fixed-order
+// reductions everywhere (no atomics), so reruns are bit-identical.
+#include "common.h"
+
+// ---------------------------------------------------------------- fill
+extern "C" __global__ void __launch_bounds__(256) k_fill_zero(float* __restrict__ p, long long n) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long stride = (long long)gridDim.x * blockDim.x;
+    for (; i < n; i += stride) p[i] = 0.f;
+}
+
+// ---------------------------------------------------------------- embedding
+// x[n, :] = E[ids[n], :]  (train_kernels.cu:724-730). Bit-exact gather.
+extern "C" __global__ void __launch_bounds__(256)
+k_embed_fwd(const float* __restrict__ E, const unsigned* __restrict__ ids, float* __restrict__ x, int rows, int D) {
+    if ((D & 3) == 0) {
+        long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;   // float4 index
+        int q = D >> 2;
+        if (i >= (long long)rows * q) return;
+        long long n = i / q;
+        int j = (int)(i - n * q);
+        ((f32x4*)x)[i] = ((const f32x4*)E)[(long long)ids[n] * q + j];
+    } else {
+        long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+        if (i >= (long long)rows * D) return;
+        long long n = i / D;
+        int j = (int)(i - n * D);
+        x[i] = E[(long long)ids[n] * D + j];
+    }
+}
+
+// dE[tok, j] += sum of dx[n, j] over the rows n holding tok, in ascending n
+// (embedding.c:4-15, train_kernels.cu:736-740).  The host groups rows by token
+// (stable counting sort): order[] lists row indices, segment s covers
+// order[seg_start[s] .. seg_start[s+1]) and belongs to token seg_tok[s].
+// One thread per (segment, column): no two threads touch the same output.
+extern "C" __global__ void __launch_bounds__(256)
+k_embed_bwd(const float* __restrict__ dx, const unsigned* __restrict__ order, const unsigned* __restrict__ seg_start,
+            const unsigned* __restrict__ seg_tok, int nseg, float* __restrict__ dE, int D) {
+    int s = blockIdx.x;
+    int j = blockIdx.y * blockDim.x + threadIdx.x;
+    if (s >= nseg || j >= D) return;
+    float* dst = dE + (long long)seg_tok[s] * D + j;
+    float acc = *dst;
+    unsigned e = seg_start[s + 1];
+    for (unsigned k = seg_start[s]; k < e; k++) acc += dx[(long long)order[k] * D + j];
+    *dst = acc;
+}
+
+// ---------------------------------------------------------------- RMSNorm
+// out = (x * r) * w with r = 1/sqrt(mean(x^2) + eps), r saved per row
+// (tensor.c:217-234, train_kernels.cu:535-547).  One wavefront per row;
+// sqrt in f64 then rounded, as the reference does.
+extern "C" __global__ void __launch_bounds__(256)
+k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w, float* __restrict__ out,
+              float* __restrict__ rinv, int rows, int cols, float eps) {
+    int row = blockIdx.x * 4 + (threadIdx.x >> 6);
+    int lane = threadIdx.x & 63;
+    if (row >= rows) return;
+    const float* xr = x + (long long)row * cols;
+    float ss = 0.f;
+    for (int i = lane; i < cols; i += 64) ss += xr[i] * xr[i];
+    ss = wave_sum(ss);
+    float ms = ss / (float)cols;
+    float r = 1.0f / (float)sqrt((double)(ms + eps));
+    if (lane == 0) rinv[row] = r;
+    float* orow = out + (long long)row * cols;
+    for (int i = lane; i < cols; i += 64) orow[i] = xr[i] * r * w[i];
+}
+
+// dx += w*r*dy - (r^3/cols)*x*S, S = sum(dy*w*x)  (model_ops.c:89-117,
+// train_kernels.cu:552-569).  The weight gradient dy*x*r is reduced over the
+// block's RMS_ROWS rows in row order and written as one partial row per
+// block; k_colsum_final adds the partials in block order.
+#define RMS_ROWS 32
+extern "C" __global__ void __launch_bounds__(256)
+k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ rinv,
+              const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ wpart, int rows, int cols) {
+    extern __shared__ float part[];   // [4][cols]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int r0 = blockIdx.x * RMS_ROWS;
+    float* mine = part + wave * cols;
+    for (int i = lane; i < cols; i += 64) mine[i] = 0.f;
+    // wave `wave` handles rows r0 + wave*8 .. +7, in order
+    for (int rr = 0; rr < RMS_ROWS / 4; rr++) {
+        int row = r0 + wave * (RMS_ROWS / 4) + rr;
+        if (row >= rows) break;
+        const float* xr = x + (long long)row * cols;
+        const float* d = dy + (long long)row * cols;
+        float* g = dx + (long long)row * cols;
+        float r = rinv[row];
+        float r3 = r * r * r;
+        float S = 0.f;
+        for (int i = lane; i < cols; i += 64) S += d[i] * w[i] * xr[i];
+        S = wave_sum(S);
+        float c = r3 / (float)cols;
+        for (int j = lane; j < cols; j += 64) {
+            g[j] += w[j] * r * d[j] - c * xr[j] * S;
+            mine[j] += d[j] * xr[j] * r;
+        }
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < cols; j += 256) {
+        float s = part[j];
+        s += part[cols + j];
+        s += part[2 * cols + j];
+        s += part[3 * cols + j];
+        wpart[(long long)blockIdx.x * cols + j] = s;
+    }
+}
+
+// ---------------------------------------------------------------- column sums
+// partial[b, c] = sum over rows [b*rpb, (b+1)*rpb) of in[r, c], rows in order.
+extern "C" __global__ void __launch_bounds__(256)
+k_colsum_partial(const float* __restrict__ in, int rows, int cols, int ld, int rpb, float* __restrict__ partial) {
+    int b = blockIdx.x;
+    int c = blockIdx.y * 256 + threadIdx.x;
+    if (c >= cols) return;
+    int r = b * rpb, e = r + rpb;
+    if (e > rows) e = rows;
+    float s = 0.f;
+    for (; r < e; r++) s += in[(long long)r * ld + c];
+    partial[(long long)b * cols + c] = s;
+}
+
+// out[c] (+)= sum_b partial[b, c] in block order (bias / norm-weight grads,
+// the role of train_kernels.cu:518-531).
+extern "C" __global__ void __launch_bounds__(256)
+k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __restrict__ out, int accumulate) {
+    int c = blockIdx.x * 256 + threadIdx.x;
+    if (c >= cols) return;
+    float s = partial[c];
+    for (int b = 1; b < nb; b++) s += partial[(long long)b * cols + c];
+    out[c] = accumulate ? out[c] + s : s;
+}
+
+// ---------------------------------------------------------------- RoPE
+// In place on the Q and K column ranges of qkv [N, ld]: pair (2k, 2k+1) of
+// head h at position t rotated by (cos, sin)[t, k] (rope.c:20-40); inverse
+// applies the transpose (model_ops.c:130-155).
+extern "C" __global__ void __launch_bounds__(256)
+k_rope_qk(float* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int N, int T,
+          int H, int hd, int ld, int inverse) {
+    int half = hd >> 1, D = H * hd;
+    long long total = (long long)N * H * half;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= total) return;
+    int k = (int)(i % half);
+    long long rest = i / half;
+    int h = (int)(rest % H);
+    long long n = rest / H;
+    int t = (int)(n % T);
+    float c = cos_t[t * half + k], s = sin_t[t * half + k];
+    float* row = qkv + n * (long long)ld;
+    int c0 = h * hd + 2 * k;
+#pragma unroll
+    for (int part = 0; part < 2; part++) {
+        float* p = row + part * D + c0;
+        float a0 = p[0], a1 = p[1];
+        if (!inverse) { p[0] = a0 * c - a1 * s; p[1] = a0 * s + a1 * c; }
+        else { p[0] = a0 * c + a1 * s; p[1] = -a0 * s + a1 * c; }
+    }
+}
+
+// ---------------------------------------------------------------- SwiGLU
+// h = (g * sigmoid(g)) * u over gu = [gate | up] (feedforward.c:146-150).
+extern "C" __global__ void __launch_bounds__(256)
+k_swiglu_fwd(const float* __restrict__ gu, float* __restrict__ h, int rows, int F) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * F) return;
+    long long n = i / F;
+    int j = (int)(i - n * F);
+    float g = gu[n * 2 * F + j], u = gu[n * 2 * F + F + j];
+    float sg = 1.0f / (1.0f + expf(-g));
+    h[i] = (g * sg) * u;
+}
+
+// Gradients of h = silu(g)*u in the reference autograd order (node.c:81-96,
+// 217-226): du = dh*silu; dg = (dh*u)*sg + ((dh*u)*g)*(sg*(1-sg)).
+extern "C" __global__ void __launch_bounds__(256)
+k_swiglu_bwd(const float* __restrict__ gu, const float* __restrict__ dh, float* __restrict__ dgu, int rows, int F) {
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long long)rows * F) return;
+    long long n = i / F;
+    int j = (int)(i - n * F);
+    float g = gu[n * 2 * F + j], u = gu[n * 2 * F + F + j];
+    float sg = 1.0f / (1.0f + expf(-g));
+    float d = dh[i];
+    float silu_g = d * u;
+    float gate = silu_g * sg + (silu_g * g) * (sg * (1.0f - sg));
+    dgu[n * 2 * F + j] = gate;
+    dgu[n * 2 * F + F + j] = d * (g * sg);
+}
+
+// ---------------------------------------------------------------- cross-entropy
+// One 256-thread block per row of logits [rows, ld] (V valid columns):
+//   loss_rows[n] = log(sum exp(z - max)) + max - z[t]      (loss.c:76-104)
+//   z <- (softmax(z) - onehot(t)) * grad_scale  if write_grad (loss.c:55-74)
+// The max/sum pass is an online (max, scaled-sum) reduction per thread,
+// combined across the block in fixed order.
+__device__ __forceinline__ void ms_combine(float& m, float& s, float m2, float s2) {
+    if (m2 > m) { s = s * expf(m - m2) + s2; m = m2; }
+    else if (m2 != -INFINITY) { s = s + s2 * expf(m2 - m); }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__ targets,
+                float* __restrict__ loss_rows, int V, float grad_scale, int write_grad) {
+    __shared__ float sm[4], ss[4];
+    const long long row = blockIdx.x;
+    float* z = logits + row * ld;
+    float m = -INFINITY, s = 0.f;
+    for (int j = threadIdx.x; j < V; j += 256) {
+        float v = z[j];
+        if (v > m) { s = s * expf(m - v) + 1.f; m = v; }
+        else s += expf(v - m);
+    }
+    // wave-level fixed-order combine
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float m2 = __shfl_xor(m, o, WAVE), s2 = __shfl_xor(s, o, WAVE);
+        float mn = fmaxf(m, m2);
+        float a = (m == -INFINITY) ? 0.f : s * expf(m - mn);
+        float b = (m2 == -INFINITY) ? 0.f : s2 * expf(m2 - mn);
+        m = mn; s = a + b;
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { sm[wave] = m; ss[wave] = s; }
+    __syncthreads();
+    float M = sm[0], S = ss[0];
+    for (int w = 1; w < 4; w++) ms_combine(M, S, sm[w], ss[w]);
+    unsigned t = targets[row];
+    float zt = z[t];
+    __syncthreads();
+    if (threadIdx.x == 0) loss_rows[row] = (float)log((double)S) + M - zt;
+    if (!write_grad) return;
+    float inv = 1.0f / S;
+    for (int j = threadIdx.x; j < V; j += 256) {
+        float p = expf(z[j] - M) * inv;
+        if (j == (int)t) p -= 1.0f;
+        z[j] = p * grad_scale;
+    }
+}
+
+// First index of the row maximum (greedy decoding; ties -> lowest index).
+extern "C" __global__ void __launch_bounds__(256)
+k_argmax_rows(const float* __restrict__ logits, int ld, int V, unsigned* __restrict__ out) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float* z = logits + (long long)blockIdx.x * ld;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int j = threadIdx.x; j < V; j += 256) {
+        float v = z[j];
+        if (v > best) { best = v; idx = j; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float v2 = __shfl_xor(best, o, WAVE);
+        int i2 = __shfl_xor(idx, o, WAVE);
+        if (v2 > best || (v2 == best && i2 < idx)) { best = v2; idx = i2; }
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int k = bi[0];
+        for (int w = 1; w < 4; w++)
+            if (bv[w] > b || (bv[w] == b && bi[w] < k)) { b = bv[w]; k = bi[w]; }
+        out[blockIdx.x] = (unsigned)k;
+    }
+}
+
+// ---------------------------------------------------------------- grad norm
+// Per-block partial sums of squares over a fixed 1024x256 grid-stride layout
+// (train_kernels.cu:777-784); the host adds the partials in f64 in order.
+extern "C" __global__ void __launch_bounds__(256)
+k_sumsq_partial(const float* __restrict__ x, long long n, float* __restrict__ partial) {
+    __shared__ float ws[4];
+    float s = 0.f;
+    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
+        s += x[i] * x[i];
+    s = wave_sum(s);
+    if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
+    __syncthreads();
+    if (threadIdx.x == 0) partial[blockIdx.x] = ((ws[0] + ws[1]) + ws[2]) + ws[3];
+}
+
+// ---------------------------------------------------------------- Adam / AdamW
+// adam_update_one (adam.c:80-95) with the clip scale of k_adam
+// (train_kernels.cu:787-800).  wd != 0 adds decoupled weight decay:
+// p -= lr*m_hat/(sqrt(v_hat)+eps) + (lr*wd)*p; wd = 0 is exactly Adam.
+// Contraction is off so each operation rounds as the CPU path does.
+__device__ __forceinline__ void adam_one(float& p, float g, float& m, float& v, float lr, float b1, float b2,
+                                         float eps, float bc1, float bc2, float gs, float lrwd) {
+#pragma clang fp contract(off)
+    float gi = g * gs;
+    float mi = b1 * m + (1.0f - b1) * gi;
+    float vi = b2 * v + (1.0f - b2) * gi * gi;
+    m = mi;
+    v = vi;
+    float mh = mi / bc1;
+    float vh = vi / bc2;
+    float upd = lr * mh / (__builtin_sqrtf(vh) + eps);
+    if (lrwd != 0.f) upd = upd + lrwd * p;
+    p = p - upd;
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, long long n,
+       float lr, float b1, float b2, float eps, float bc1, float bc2, float grad_scale, float lrwd) {
+    long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    long long nq = n >> 2;
+    if (q < nq) {
+        f32x4 pp = ((f32x4*)p)[q], gg = ((const f32x4*)g)[q], mm = ((f32x4*)m)[q], vv = ((f32x4*)v)[q];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float a = pp[e], b = mm[e], c = vv[e];
+            adam_one(a, gg[e], b, c, lr, b1, b2, eps, bc1, bc2, grad_scale, lrwd);
+            pp[e] = a; mm[e] = b; vv[e] = c;
+        }
+        ((f32x4*)p)[q] = pp; ((f32x4*)m)[q] = mm; ((f32x4*)v)[q] = vv;
+    }
+    long long tail = nq * 4 + q;
+    if (q < (n & 3)) {
+        float a = p[tail], b = m[tail], c = v[tail];
+        adam_one(a, g[tail], b, c, lr, b1, b2, eps, bc1, bc2, grad_scale, lrwd);
+        p[tail] = a; m[tail] = b; v[tail] = c;
+    }
+}
