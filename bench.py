@@ -1,0 +1,260 @@
+"""bench.py -- MI355X GPU matmul path of turkce-llm, one JSON line.
+
+Headline (BASELINE.json metric, configs[1]): the fp32 GEMM sweep at the
+model's real shapes with M = B*T = 8192 -- QKV, attention-out, gate/up
+(fused, N = 2F), down and the 31,769-wide tied LM head, each as forward
+(NN, LM head NT), dX (NT / NN for the head) and dW (TN).  One "step" is one
+pass over all fifteen GEMMs with operands resident in HBM.  value = sweep
+FLOPs / sweep time (TFLOP/s), against the 157.3 TFLOP/s FP32-MFMA peak.
+
+Also reported (same run, same library): forward tokens/s (config 3: B=8,
+T=1024, forward + mean cross-entropy) and training tokens/s (config 4:
+forward, CE, full backward and AdamW with lr 3e-4, betas 0.9/0.95,
+eps 1e-8, wd 0.1), with random-init weights of the real architecture.
+
+roofline: the LM-head forward GEMM (the largest single kernel), algorithmic
+2*M*N*K FLOPs per launch divided by its average launch time measured here
+with HIP events on the library's stream.
+
+cpu_baseline: the reference's own CPU matmul (tensor_matmul2d, built from
+/root/reference into oracle/_ref) on a bounded sample of the sweep; falls
+back to the oracle restatement when oracle/_ref was not built.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+PEAK_FP32_MFMA = 157.3   # TFLOP/s, MI355X dense FP32 matrix
+PEAK_HBM = 8000.0        # GB/s
+V, D, H, L, F = 31769, 384, 6, 12, 1024
+B, T = 8, 1024
+M = B * T
+METRIC = "GEMM TFLOP/s (% FP32-MFMA peak); fwd+train tokens/s, 33.5M LM, B8 T1024"
+
+# name, forward N, K   (forward: [M,K] x [K,N])
+SHAPES = [("qkv", 3 * D, D), ("attn_out", D, D), ("gate_up", 2 * F, D), ("down", D, F), ("lm_head", V, D)]
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def load_trlm():
+    import importlib.util
+    spec = importlib.util.spec_from_file_location("trlm_amd", os.path.join(ROOT, "turkce-llm_amd", "trlm.py"))
+    mod = importlib.util.module_from_spec(spec)
+    sys.modules["trlm_amd"] = mod
+    spec.loader.exec_module(mod)
+    return mod
+
+
+class Sweep:
+    """Device operands of the fifteen GEMMs and their launches."""
+
+    def __init__(self, trlm, dev):
+        self.dev = dev
+        rng = np.random.default_rng(2026)
+        self.items = []
+        self.bufs = []
+        for name, N, K in SHAPES:
+            ldn = (N + 3) // 4 * 4
+            X = rng.standard_normal((M, K), dtype=np.float32)                 # activations N(0,1)
+            if name == "lm_head":
+                W = (0.02 * rng.standard_normal((N, K), dtype=np.float32))   # E [V, D]
+            else:
+                W = (0.02 * rng.standard_normal((K, N), dtype=np.float32))   # W [K, N]
+            dY = rng.standard_normal((M, ldn), dtype=np.float32)
+            dX, dW, dWb = dev.upload(X), dev.upload(W), dev.upload(dY)
+            dOut = dev.empty(M * ldn * 4)
+            dGX = dev.empty(M * K * 4)
+            dGW = dev.empty(N * K * 4)
+            self.bufs += [dX, dW, dWb, dOut, dGX, dGW]
+            fl = 2.0 * M * N * K
+            if name == "lm_head":
+                # logits = X @ E^T (NT); dX = dY @ E (NN, K = V); dE = dY^T @ X (TN, K = M)
+                self.items.append((name + "_fwd", fl, (0, 1, dX, dW, dOut, M, N, K, K, K, ldn)))
+                self.items.append((name + "_dx", fl, (0, 0, dWb, dW, dGX, M, K, N, ldn, K, K)))
+                self.items.append((name + "_dw", fl, (1, 0, dWb, dX, dGW, N, K, M, ldn, K, K)))
+            else:
+                # Y = X @ W (NN); dX = dY @ W^T (NT); dW = X^T @ dY (TN, K = M)
+                self.items.append((name + "_fwd", fl, (0, 0, dX, dW, dOut, M, N, K, K, N, ldn)))
+                self.items.append((name + "_dx", fl, (0, 1, dWb, dW, dGX, M, K, N, ldn, N, K)))
+                self.items.append((name + "_dw", fl, (1, 0, dX, dWb, dGW, K, N, M, K, ldn, N)))
+        self.flops = sum(f for _, f, _ in self.items)
+
+    def run(self, item):
+        ta, tb, A, Bm, Cm, m, n, k, lda, ldb, ldc = item[2]
+        self.dev.matmul(ta, tb, A, Bm, Cm, m, n, k, lda, ldb, ldc)
+
+    def step(self):
+        for it in self.items:
+            self.run(it)
+
+    def close(self):
+        for p in self.bufs:
+            self.dev.free(p)
+
+
+def time_events(hip, fn, reps):
+    from ctypes import byref
+    import trlm_amd
+    t = trlm_amd.TrlmTimer()
+    hip.trlm_timer_create(byref(t))
+    hip.trlm_timer_start(byref(t))
+    for _ in range(reps):
+        fn()
+    ms = hip.trlm_timer_stop_ms(byref(t))
+    hip.trlm_timer_destroy(byref(t))
+    return ms / reps
+
+
+def model_params(rng):
+    """Random-init weights of the real architecture (lm_init's layout and
+    scales: matrices N(0, 0.02), biases 0, norm weights 1)."""
+    parts = [0.02 * rng.standard_normal(V * D, dtype=np.float32)]
+    for _ in range(L):
+        parts += [np.ones(D, np.float32), 0.02 * rng.standard_normal(D * 3 * D, dtype=np.float32),
+                  np.zeros(3 * D, np.float32), 0.02 * rng.standard_normal(D * D, dtype=np.float32),
+                  np.zeros(D, np.float32), np.ones(D, np.float32),
+                  0.02 * rng.standard_normal(D * 2 * F, dtype=np.float32), np.zeros(2 * F, np.float32),
+                  0.02 * rng.standard_normal(F * D, dtype=np.float32), np.zeros(D, np.float32)]
+    parts.append(np.ones(D, np.float32))
+    return np.concatenate(parts).astype(np.float32)
+
+
+def model_benchmarks(trlm, steps, warmup):
+    rng = np.random.default_rng(7)
+    params = model_params(rng)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, B, T)
+    adam = trlm.Adam(hm, 3e-4, 0.9, 0.95, 1e-8)
+    ids = rng.integers(0, V, M, dtype=np.uint32)
+    tgt = rng.integers(0, V, M, dtype=np.uint32)
+    out = {}
+    try:
+        for _ in range(warmup):
+            tr.eval_loss(ids, tgt)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = tr.eval_loss(ids, tgt)
+        fwd = (time.perf_counter() - t0) / steps
+        for _ in range(warmup):
+            tr.forward_backward(ids, tgt)
+            tr.adamw_step(adam, 0.1)
+        t0 = time.perf_counter()
+        for _ in range(steps):
+            loss = tr.forward_backward(ids, tgt)
+            tr.adamw_step(adam, 0.1)
+        trn = (time.perf_counter() - t0) / steps
+        out = {"fwd_ms": fwd * 1e3, "fwd_tokens_per_s": M / fwd, "train_ms": trn * 1e3,
+               "train_tokens_per_s": M / trn, "train_loss_last": float(loss),
+               "fwd_tflops_algorithmic": 625.16e9 / fwd / 1e12, "train_tflops_algorithmic": 1875.5e9 / trn / 1e12}
+    finally:
+        tr.destroy()
+        hm.close()
+    return out
+
+
+def cpu_baseline(seconds_target=10.0):
+    """Reference tensor_matmul2d (or the oracle) on QKV-shaped rows."""
+    import oracle
+    rng = np.random.default_rng(1)
+    K, N = D, 3 * D
+    Wq = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
+    kind = "reference" if oracle.reference_available() else "port"
+    rows = 64
+    while True:
+        X = rng.standard_normal((rows, K)).astype(np.float32)
+        out = np.zeros((rows, N), np.float32)
+        if kind == "reference":
+            ref = oracle.Reference()
+            dt = ref.h.refh_time_matmul(rows, N, K, X, Wq, out)
+        else:
+            t0 = time.perf_counter()
+            oracle.matmul(X, Wq)
+            dt = time.perf_counter() - t0
+        if dt * 2 >= seconds_target or rows >= M:
+            break
+        rows = min(M, int(rows * max(2.0, seconds_target / max(dt, 1e-3) * 0.6)))
+    tflops = 2.0 * rows * N * K / dt / 1e12
+    return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": kind,
+            "sample": "QKV forward GEMM rows 0..%d (%dx%dx%d) through %s, %.1f s" % (
+                rows - 1, rows, N, K, "tensor_matmul2d (oracle/_ref)" if kind == "reference"
+                else "the oracle's reference-order matmul", dt)}
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-model", action="store_true", help="skip the forward/training measurements")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
+              "(RCCL data parallel) is not implemented (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+        sys.exit(2)
+
+    trlm = load_trlm()
+    _, hip = trlm.libs()
+    dev = trlm.Device()
+    sweep = Sweep(trlm, dev)
+    log("sweep: %d GEMMs, %.1f GFLOP per step" % (len(sweep.items), sweep.flops / 1e9))
+    for _ in range(args.warmup):
+        sweep.step()
+    dev.sync()
+    total_ms = time_events(hip, sweep.step, args.steps)
+    per_gemm = {}
+    variants = {}
+    for it in sweep.items:
+        ms = time_events(hip, lambda it=it: sweep.run(it), max(3, args.steps // 2))
+        per_gemm[it[0]] = round(it[1] / (ms * 1e-3) / 1e12, 2)
+        sweep.run(it)
+        variants[it[0]] = "%s/split%d" % dev.last_variant()
+    log("per-GEMM TFLOP/s: %s" % per_gemm)
+    # dominant kernel: the LM-head forward GEMM, one launch = one kernel
+    head = [it for it in sweep.items if it[0] == "lm_head_fwd"][0]
+    head_ms = time_events(hip, lambda: sweep.run(head), max(5, args.steps))
+    achieved = head[1] / (head_ms * 1e-3) / 1e12
+    sweep.close()
+    dev.close()
+
+    value = sweep.flops / (total_ms * 1e-3) / 1e12
+    line = {
+        "metric": METRIC, "value": round(value, 3), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(total_ms, 4), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+        "config": {"workload": "fp32 GEMM sweep at model shapes (configs[1]): QKV, attn-out, gate_up, down, "
+                               "LM head x (fwd, dX, dW), M=B*T=8192", "global_batch": B, "seq_len": T,
+                   "parallelism": "single-gpu"},
+        "pct_fp32_mfma_peak": round(100.0 * value / PEAK_FP32_MFMA, 2),
+        "gemm_tflops": per_gemm, "gemm_variant": variants,
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "kernel": "%s (LM head fwd 8192x31769x384 NT)" % variants["lm_head_fwd"],
+                     "launch_ms": round(head_ms, 4)},
+    }
+    if not args.no_model:
+        log("model: forward / train at B=%d T=%d" % (B, T))
+        line.update({k: (round(v, 3) if isinstance(v, float) else v)
+                     for k, v in model_benchmarks(trlm, max(3, args.steps // 2), args.warmup).items()})
+    if not args.no_cpu:
+        log("cpu baseline leg")
+        cb = cpu_baseline()
+        line["cpu_baseline"] = {"value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
+                                "sample": cb["sample"]}
+        line["gpu_vs_cpu_gemm"] = round(value / cb["value"], 1)
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()
