@@ -191,13 +191,45 @@ def cpu_baseline(seconds_target=10.0):
                 else "the oracle's reference-order matmul", dt)}
 
 
+def summarize_profile(path):
+    """Print per-kernel statistics from a rocprofv3 run (--kernel-trace
+    --output-format csv): one line per (kernel, grid) so that the LM-head
+    dispatches of the NT GEMM stand apart from the other NT shapes."""
+    import csv
+    import glob
+    files = glob.glob(os.path.join(path, "**", "*kernel_trace.csv"), recursive=True)
+    if not files:
+        sys.exit("no *kernel_trace.csv under %s" % path)
+    groups = {}
+    for f in files:
+        with open(f) as fh:
+            for r in csv.DictReader(fh):
+                name = r.get("Kernel_Name") or r.get("kernel_name")
+                dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+                grid = (r.get("Grid_Size_X") or r.get("Grid_Size", "?"), r.get("Grid_Size_Y", ""),
+                        r.get("Grid_Size_Z", ""))
+                key = (name, "x".join(g for g in grid if g))
+                groups.setdefault(key, []).append(dur)
+    total = sum(sum(v) for v in groups.values())
+    print("%-36s %-22s %7s %12s %12s %7s" % ("kernel", "grid (work-items)", "calls", "total_us", "avg_us", "pct"))
+    for (name, grid), v in sorted(groups.items(), key=lambda kv: -sum(kv[1])):
+        print("%-36s %-22s %7d %12.1f %12.2f %6.2f%%" % (name[:36], grid, len(v), sum(v) / 1e3,
+                                                          sum(v) / len(v) / 1e3, 100.0 * sum(v) / total))
+
+
 def main():
+    if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
+        summarize_profile(sys.argv[2])
+        return
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-model", action="store_true", help="skip the forward/training measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--model-only", action="store_true",
+                    help="only the B8 T1024 forward/train measurements (for focused profiling); "
+                         "prints them as a JSON line without the sweep")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
@@ -206,6 +238,9 @@ def main():
 
     trlm = load_trlm()
     _, hip = trlm.libs()
+    if args.model_only:
+        print(json.dumps(model_benchmarks(trlm, args.steps, args.warmup)), flush=True)
+        return
     dev = trlm.Device()
     sweep = Sweep(trlm, dev)
     log("sweep: %d GEMMs, %.1f GFLOP per step" % (len(sweep.items), sweep.flops / 1e9))

@@ -426,7 +426,9 @@ static void seq_alloc(Seq* s, const OrCfg* c, uint32_t T, const float* P, const 
     s->x_fin = (float*)xcalloc(T * D);
     s->nf = (float*)xcalloc(T * D);
     s->logits = (float*)xcalloc((uint64_t)T * V);
-    uint64_t big = V * D; if (2 * F * D > big) big = 2 * F * D;
+    uint64_t big = V * D;
+    if (2 * F * D > big) big = 2 * F * D;
+    if (3 * D * D > big) big = 3 * D * D;
     s->tmpT = (float*)xcalloc(big);
 }
 

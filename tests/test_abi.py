@@ -1,0 +1,171 @@
+"""The drop-in C ABI, checked without a GPU.
+
+  - every function declared in include/*.h is exported by the built
+    libraries (gpu_train.h / gpu_ops.h / hip_backend.h / trlm_ext.h by
+    libtrlm_hip.so, trlm_host.h by libtrlm_host.so);
+  - libtrlm_hip.so leaves undefined only the reference-runtime symbols the
+    reference's own gpu_train.c / gpu_ops.c use (so the reference's objects
+    can provide them) plus libc / HIP runtime;
+  - the gfx950 code object holds every kernel the host code looks up;
+  - the Python structure mirror matches the C compiler's layout;
+  - the host-side logic of the path is bit-identical to the oracle: PCG,
+    scalar maths feeding RoPE and Adam, RoPE tables, batch sampling.
+No GPU call is made here (HIP calls without a device would end the process).
+"""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+INC = os.path.join(ROOT, "include")
+
+PROTO = re.compile(r"^\s*(?:const\s+)?[A-Za-z_][A-Za-z0-9_]*\s*\**\s+\**\s*([a-z_][a-z0-9_]*)\s*\(", re.M)
+
+
+def declared(header):
+    with open(os.path.join(INC, header)) as fh:
+        text = fh.read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    names = set(PROTO.findall(text))
+    return {n for n in names if n not in ("if", "while", "for", "return", "sizeof")}
+
+
+def test_headers_declare_the_reference_api():
+    train = declared("gpu_train.h")
+    assert {"gpu_trainer_create", "gpu_trainer_destroy", "gpu_trainer_upload", "gpu_trainer_download",
+            "gpu_trainer_download_grads", "gpu_trainer_upload_grads", "gpu_trainer_sample_batch",
+            "gpu_trainer_forward_backward", "gpu_trainer_eval_loss", "gpu_trainer_grad_norm",
+            "gpu_trainer_adam_step", "gpu_trainer_adam_step_scaled"} <= train
+    ops = declared("gpu_ops.h")
+    assert {"gpu_ops_init", "gpu_ops_shutdown", "gpu_ops_init_workers", "gpu_ops_set_worker_id",
+            "node_matmul2d_gpu", "gpu_ops_debug_stats", "gpu_ops_debug_reset"} <= ops
+
+
+def test_every_declared_symbol_is_exported(trlm):
+    host, hip = trlm.libs()
+    for header, lib in [("gpu_train.h", hip), ("gpu_ops.h", hip), ("hip_backend.h", hip), ("trlm_ext.h", hip),
+                        ("trlm_host.h", host)]:
+        for name in declared(header):
+            assert hasattr(lib, name), (header, name)
+
+
+def test_reference_prototypes_unchanged():
+    """The prototypes of the reference's model/gpu_train.h:86-125 and
+    model/gpu_ops.h:23-60, as text, appear unchanged in include/."""
+    want = [
+        "GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,\n"
+        "                              Node** params, u32 num_params, u32 batch_size, u32 seq_len);",
+        "void gpu_trainer_destroy(GpuTrainer* g);",
+        "void gpu_trainer_upload(GpuTrainer* g, Node** params, const AdamOptimizer* opt);",
+        "void gpu_trainer_download(GpuTrainer* g, Node** params, AdamOptimizer* opt);",
+        "void gpu_trainer_download_grads(GpuTrainer* g, Node** params);",
+        "void gpu_trainer_upload_grads(GpuTrainer* g, Node** params);",
+        "void gpu_trainer_sample_batch(const u32* tokens, u64 num_tokens, u32 seq_len, u32 batch_size,\n"
+        "                              u64 seed_base, u32* ids_out, u32* targets_out);",
+        "f32 gpu_trainer_forward_backward(GpuTrainer* g, const u32* ids, const u32* targets);",
+        "f32 gpu_trainer_eval_loss(GpuTrainer* g, const u32* ids, const u32* targets);",
+        "f64 gpu_trainer_grad_norm(GpuTrainer* g);",
+        "void gpu_trainer_adam_step(GpuTrainer* g, AdamOptimizer* opt);",
+        "void gpu_trainer_adam_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 grad_scale);",
+        "#define GPU_TRAIN_MAX_PARAMS (LM_MAX_LAYERS * 10u + 2u)",
+        "#define GPU_TRAIN_NORM_BLOCKS 1024u",
+    ]
+    text = open(os.path.join(INC, "gpu_train.h")).read()
+    for w in want:
+        assert w in text, w
+    ops = open(os.path.join(INC, "gpu_ops.h")).read()
+    for w in ["void gpu_ops_init(Allocator* scratch, const char* ptx_path);", "void gpu_ops_shutdown(void);",
+              "void gpu_ops_init_workers(Allocator* scratch, const char* ptx_path, u32 num_workers);",
+              "void gpu_ops_set_worker_id(i32 worker_id);", "Node* node_matmul2d_gpu(Allocator* alloc, Node* a, Node* b);",
+              "void gpu_ops_debug_stats(f64* out_total_seconds, u32* out_call_count);",
+              "void gpu_ops_debug_reset(void);"]:
+        assert w in ops, w
+
+
+def test_undefined_symbols_are_runtime_only(trlm):
+    out = subprocess.run(["nm", "-D", "--undefined-only", trlm.LIB_HIP], capture_output=True, text=True,
+                         check=True).stdout
+    names = {ln.split()[-1].split("@")[0] for ln in out.splitlines() if ln.strip()}
+    runtime = {"allocator_alloc", "tensor_create", "tensor_transpose", "tensor_contiguous", "tensor_add_inplace",
+               "node_make_custom", "rope_build_tables", "pcg_seed", "pcg_range_i64", "m_powf", "m_sqrt",
+               "m_sqrtf"}
+    other = {n for n in names if not (n.startswith("hip") or n.startswith("_") or n in runtime)}
+    libc = {"fprintf", "fflush", "_exit", "fopen", "fseek", "ftell", "fread", "fclose", "malloc", "calloc",
+            "realloc", "free", "memset", "memcpy", "snprintf", "stderr", "stdout", "clock_gettime",
+            "pthread_mutex_lock", "pthread_mutex_unlock", "pthread_mutex_init", "pthread_mutex_destroy"}
+    assert other <= libc, other - libc
+    assert runtime & names == runtime, runtime - names
+
+
+def test_code_object_has_every_kernel(trlm):
+    with open(trlm.KERNELS, "rb") as fh:
+        blob = fh.read()
+    src = ""
+    for f in ("gpu_train.c", "trlm_gemm.c"):
+        src += open(os.path.join(ROOT, "turkce-llm_amd", "csrc", f)).read()
+    names = set(re.findall(r'"(k_[a-z0-9_]+)"', src))
+    names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in ("128x128", "64x128", "64x64")}
+    names |= {"k_gemm_%s_64x64_u" % l for l in ("nn", "nt", "tn", "tt")}
+    for n in sorted(names):
+        assert n.encode() + b"\0" in blob, n
+
+
+def test_structure_layout(trlm):
+    ok, got, want = trlm.check_layout()
+    assert ok, (got, want)
+    _, hip = trlm.libs()
+    assert hip.trlm_sizeof_hip_ctx() == C.sizeof(trlm.HipCtx)
+
+
+def test_host_runtime_matches_oracle(trlm, orc):
+    host, hip = trlm.libs()
+    L = orc.lib()
+    r1 = host.pcg_seed(4242, 7)
+    r2 = orc.pcg_stream(4242, 7)
+    for _ in range(50):
+        assert host.pcg_range_i64(C.byref(r1), 0, 31769) == L.or_pcg_range_i64(C.byref(r2), 0, 31769)
+    for _ in range(20):
+        assert float(host.pcg_gaussian(C.byref(r1), 0.0, 0.02)).hex() == \
+            float(L.or_pcg_gaussian(C.byref(r2), 0.0, 0.02)).hex()
+    rng = np.random.default_rng(1)
+    for x in rng.uniform(1e-8, 1e8, 200):
+        assert float(host.m_sqrt(x)).hex() == float(L.or_m_sqrt(x)).hex()
+    for b in (0.9, 0.95, 0.999):
+        for t in range(1, 200, 7):
+            assert np.float32(host.m_powf(b, float(t))) == np.float32(L.or_m_powf(b, float(t)))
+    for x in rng.uniform(-1100, 1100, 200):
+        assert np.float32(host.m_sinf(x)) == np.float32(L.or_m_sinf(x))
+        assert np.float32(host.m_cosf(x)) == np.float32(L.or_m_cosf(x))
+
+
+@pytest.mark.parametrize("T,hd", [(128, 64), (1024, 64), (12, 16), (100, 32)])
+def test_rope_tables_bit_exact(trlm, orc, T, hd):
+    host, _ = trlm.libs()
+    alloc = host.allocator_create(1 << 26)
+    try:
+        sh = (C.c_uint64 * 2)(T, hd // 2)
+        ct = host.tensor_create(C.byref(alloc), sh, 2)
+        st = host.tensor_create(C.byref(alloc), sh, 2)
+        host.rope_build_tables(C.byref(ct), C.byref(st), T, hd, 10000.0)
+        c, s = orc.rope_tables(T, hd)
+        assert np.array_equal(trlm.tensor_np(ct).view(np.uint32), c.ravel().view(np.uint32))
+        assert np.array_equal(trlm.tensor_np(st).view(np.uint32), s.ravel().view(np.uint32))
+    finally:
+        host.allocator_destroy(C.byref(alloc))
+
+
+@pytest.mark.parametrize("T,B,seed", [(12, 5, 2026), (128, 4, 7), (1024, 8, 2026 + 99)])
+def test_sample_batch_bit_exact(trlm, orc, T, B, seed):
+    _, hip = trlm.libs()
+    toks = orc.random_tokens(50000, 31769)
+    ids = np.zeros(B * T, np.uint32)
+    tgt = np.zeros(B * T, np.uint32)
+    hip.gpu_trainer_sample_batch(toks, len(toks), T, B, seed, ids, tgt)
+    wi, wt = orc.sample_batch(toks, T, B, seed)
+    assert np.array_equal(ids, wi) and np.array_equal(tgt, wt)

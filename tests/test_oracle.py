@@ -1,0 +1,240 @@
+"""Pins the CPU oracle (oracle/trlm_oracle.c) before anything is checked
+against it.  CPU only.
+
+  - PCG32: the published pcg32 demo vector (seed 42, stream 54);
+  - scalar maths: the reference's own known answers (test_mathlib.c:33-83)
+    and libm on random points (the oracle's f64 Taylor/Newton methods are
+    accurate to a few ulp);
+  - every output of the compiled reference (oracle/_ref) frozen in
+    tests/golden/ by make_golden.py: lm_init bits, logits, loss, gradients
+    and an Adam step (small off-grid case), SHA-256 of the real model's init
+    and RoPE tables, the real-scale loss and gradient sums -- bit for bit;
+  - live bit-equality with oracle/_ref on further shapes when it is built;
+  - mathematics alone: central-difference gradients of the whole model,
+    fp64 brute-force matmul, exact small-integer matmul, Adam's closed form.
+"""
+import ctypes as C
+import hashlib
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def sha(a):
+    return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8)).hexdigest()
+
+
+@pytest.fixture(scope="module")
+def scalars():
+    with open(os.path.join(GOLDEN, "ref_scalars.json")) as fh:
+        return json.load(fh)
+
+
+@pytest.fixture(scope="module")
+def small():
+    return dict(np.load(os.path.join(GOLDEN, "ref_small.npz")))
+
+
+def test_pcg32_published_vector(orc):
+    r = orc.pcg_stream(42, 54)
+    got = [orc.lib().or_pcg_next_u32(C.byref(r)) for _ in range(6)]
+    assert got == [0xa15c02b7, 0x7b47f409, 0xba1d3330, 0x83d2f293, 0xbfa4784b, 0xcbed606e]
+
+
+def test_pcg_streams_match_reference(orc, scalars):
+    r = orc.pcg_stream(42, 54)
+    assert [orc.lib().or_pcg_next_u32(C.byref(r)) for _ in range(8)] == scalars["pcg_u32_42_54"]
+    r = orc.pcg_stream(4242, 7)
+    got = [orc.lib().or_pcg_range_i64(C.byref(r), 0, 31768) for _ in range(16)]
+    assert got == scalars["pcg_range_4242_7_0_31768"]
+    r = orc.pcg_stream(1337, 1)
+    got = [float(orc.lib().or_pcg_gaussian(C.byref(r), 0.0, 1.0)).hex() for _ in range(8)]
+    assert got == scalars["pcg_gauss_1337_1"]
+
+
+def test_mathlib_known_answers(orc):
+    L = orc.lib()
+    cases = [(L.or_m_sqrt(4.0), 2.0, 1e-12), (L.or_m_sqrt(2.0), 1.4142135623730951, 1e-12),
+             (L.or_m_sqrt(0.25), 0.5, 1e-12), (L.or_m_sqrt(1e6), 1000.0, 1e-9), (L.or_m_sqrt(0.0), 0.0, 1e-15),
+             (L.or_m_exp(0.0), 1.0, 1e-12), (L.or_m_exp(1.0), 2.718281828459045, 1e-12),
+             (L.or_m_exp(-1.0), 0.36787944117144233, 1e-12), (L.or_m_exp(10.0), 22026.465794806718, 1e-6),
+             (L.or_m_exp(-10.0), 0.0000453999297624848, 1e-15), (L.or_m_log(1.0), 0.0, 1e-12),
+             (L.or_m_log(2.718281828459045), 1.0, 1e-12), (L.or_m_log(2.0), 0.6931471805599453, 1e-12),
+             (L.or_m_log(100.0), 4.605170185988091, 1e-11), (L.or_m_log(L.or_m_exp(3.0)), 3.0, 1e-10),
+             (L.or_m_pow(2.0, 10.0), 1024.0, 1e-9), (L.or_m_pow(2.0, 0.5), 1.4142135623730951, 1e-9),
+             (L.or_m_pow(-2.0, 3.0), -8.0, 1e-9), (L.or_m_pow(-2.0, 2.0), 4.0, 1e-9),
+             (L.or_m_pow(5.0, 0.0), 1.0, 1e-12), (L.or_m_sin(0.0), 0.0, 1e-12),
+             (L.or_m_sin(math.pi / 2), 1.0, 1e-12), (L.or_m_sin(math.pi / 6), 0.5, 1e-12),
+             (L.or_m_sin(math.pi), 0.0, 1e-11), (L.or_m_cos(0.0), 1.0, 1e-12),
+             (L.or_m_cos(math.pi / 3), 0.5, 1e-12), (L.or_m_cos(math.pi), -1.0, 1e-11),
+             (L.or_m_sqrtf(2.0), 1.4142135623730951, 1e-6), (L.or_m_expf(1.0), 2.718281828459045, 1e-6),
+             (L.or_m_sinf(math.pi / 6), 0.5, 1e-6)]
+    for got, want, tol in cases:
+        assert abs(got - want) <= tol, (got, want)
+    x = 1.234
+    assert abs(L.or_m_sin(x) ** 2 + L.or_m_cos(x) ** 2 - 1.0) < 1e-12
+
+
+def test_mathlib_against_libm(orc):
+    L = orc.lib()
+    rng = np.random.default_rng(0)
+    for x in rng.uniform(1e-6, 1e6, 300):
+        assert abs(L.or_m_sqrt(x) - math.sqrt(x)) <= 4.5e-16 * math.sqrt(x)   # 2 ulp
+        assert abs(L.or_m_log(x) - math.log(x)) <= 1e-15 * max(1.0, abs(math.log(x)))
+    for x in rng.uniform(-700, 700, 300):
+        # r = x - k*ln2 with one double ln2: relative error grows ~ k * 1e-17
+        assert abs(L.or_m_exp(x) - math.exp(x)) <= 1e-13 * math.exp(x)
+    for x in rng.uniform(-2000, 2000, 300):
+        assert abs(L.or_m_sin(x) - math.sin(x)) <= 1e-12
+        assert abs(L.or_m_cos(x) - math.cos(x)) <= 1e-12
+    for b, e in zip(rng.uniform(1e-3, 1e4, 100), rng.uniform(-5, 5, 100)):
+        assert abs(L.or_m_pow(b, e) - b ** e) <= 1e-13 * b ** e
+
+
+def test_mathlib_bits_match_reference(orc, scalars):
+    L = orc.lib()
+    fn = {"sqrt": L.or_m_sqrt, "exp": L.or_m_exp, "log": L.or_m_log, "sin": L.or_m_sin, "cos": L.or_m_cos,
+          "sqrtf": L.or_m_sqrtf, "expf": L.or_m_expf, "logf": L.or_m_logf, "sinf": L.or_m_sinf,
+          "cosf": L.or_m_cosf}
+    for name, f in fn.items():
+        for x, want in scalars["math"][name]:
+            assert float(f(x)).hex() == want, (name, x)
+    for a, b, want in scalars["math"]["pow"]:
+        assert float(L.or_m_pow(a, b)).hex() == want
+    for a, b, want in scalars["math"]["powf"]:
+        assert float(L.or_m_powf(a, b)).hex() == want
+
+
+def test_rope_tables_match_reference(orc, scalars):
+    for T, hd in [(128, 64), (1024, 64), (12, 16)]:
+        c, s = orc.rope_tables(T, hd)
+        assert [sha(c), sha(s)] == scalars["rope_%d_%d" % (T, hd)]
+
+
+def test_small_case_matches_reference_fixture(orc, small):
+    """The first case of test_gpu_train.c on the oracle, bit for bit."""
+    m = orc.Model(50, 32, 2, 2, 48)
+    p = m.init(1337, 1)
+    assert np.array_equal(p.view(np.uint32), small["params"].view(np.uint32))
+    toks = orc.random_tokens(4000, 50)
+    ids, tgt = orc.sample_batch(toks, 12, 5, 2026)
+    assert np.array_equal(ids, small["ids"]) and np.array_equal(tgt, small["tgt"])
+    logits = m.forward_logits(p, ids, 5, 12)
+    assert np.array_equal(logits.view(np.uint32), small["logits"].view(np.uint32))
+    loss, grads, _ = m.forward_backward(p, ids, tgt, 5, 12)
+    assert np.float32(loss).view(np.uint32) == small["loss"].view(np.uint32)
+    assert np.array_equal(grads.view(np.uint32), small["grads"].view(np.uint32))
+    pa, ma, va = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam_step(pa, grads, ma, va, 1, 3e-4, 0.9, 0.999, 1e-8)
+    for got, key in ((pa, "adam_p"), (ma, "adam_m"), (va, "adam_v")):
+        assert np.array_equal(got.view(np.uint32), small[key].view(np.uint32)), key
+
+
+def test_real_scale_matches_reference_fixture(orc, scalars):
+    """The real model (33.5M parameters): init bits, and the real-scale case
+    (V31769 D384 H6 L12 F1024 T128 B4) loss and gradients, bit for bit."""
+    m = orc.Model(31769, 384, 6, 12, 1024)
+    assert m.total == scalars["real_num_params"] == 33490176
+    p = m.init(1337, 1)
+    assert sha(p) == scalars["real_init_sha256"]
+    toks = orc.random_tokens(200000, 31769)
+    ids, tgt = orc.sample_batch(toks, 128, 4, 2026)
+    assert sha(ids) == scalars["real_ids_sha256"]
+    loss, grads, _ = m.forward_backward(p, ids, tgt, 4, 128)
+    assert float(loss).hex() == scalars["real_loss_hex"]
+    assert sha(grads) == scalars["real_grad_sha256"]
+    # initial loss of a random model is close to ln V (PROJE_PLANI.md:340)
+    assert abs(float(loss) - math.log(31769)) < 0.2
+
+
+@pytest.mark.skipif(not __import__("oracle").reference_available(), reason="oracle/_ref not built")
+@pytest.mark.parametrize("V,D,H,L,F,T,B", [(37, 16, 1, 1, 20, 7, 3), (61, 48, 3, 2, 40, 33, 2),
+                                           (128, 64, 4, 1, 96, 64, 2)])
+def test_oracle_matches_compiled_reference(orc, V, D, H, L, F, T, B):
+    ref = orc.Reference()
+    m = orc.Model(V, D, H, L, F)
+    p = m.init(99, 3)
+    assert np.array_equal(p.view(np.uint32), ref.lm_init(m, 99, 3).view(np.uint32))
+    toks = orc.random_tokens(3000, V, 5, 6)
+    ids, tgt = orc.sample_batch(toks, T, B, 11)
+    a = m.forward_logits(p, ids, B, T)
+    b = ref.forward_logits(m, p, ids, B, T)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    la, ga, _ = m.forward_backward(p, ids, tgt, B, T)
+    lb, gb = ref.forward_backward(m, p, ids, tgt, B, T)
+    assert np.float32(la).view(np.uint32) == np.float32(lb).view(np.uint32)
+    assert np.array_equal(ga.view(np.uint32), gb.view(np.uint32))
+
+
+def test_gradients_central_difference(orc):
+    """Analytic gradients of the oracle against central differences of its
+    own loss (eps 1e-2; tolerance 0.02 + 5% as test_lm_model.c:54-119), on a
+    sample of entries of every parameter tensor of a tiny model."""
+    m = orc.Model(13, 8, 2, 1, 12)
+    p = m.init(7, 7)
+    rng = np.random.default_rng(3)
+    p = p + (0.05 * rng.standard_normal(p.size)).astype(np.float32)   # make biases/norms non-trivial
+    ids = rng.integers(0, 13, 10).astype(np.uint32)
+    tgt = rng.integers(0, 13, 10).astype(np.uint32)
+    _, g, _ = m.forward_backward(p, ids, tgt, 2, 5, nthreads=1)
+    eps = 1e-2
+    for off, n in zip(m.offsets, m.numels):
+        for k in rng.choice(int(n), min(3, int(n)), replace=False):
+            i = int(off) + int(k)
+            q = p.copy()
+            q[i] += eps
+            lp, _, _ = m.forward_backward(q, ids, tgt, 2, 5, want_grads=False, nthreads=1)
+            q[i] -= 2 * eps
+            lm, _, _ = m.forward_backward(q, ids, tgt, 2, 5, want_grads=False, nthreads=1)
+            num = (float(lp) - float(lm)) / (2 * eps)
+            assert abs(num - g[i]) <= 0.02 + 0.05 * abs(num), (i, num, g[i])
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 1, 1), (65, 33, 17), (3, 200, 129), (128, 70, 384)])
+def test_matmul_against_fp64(orc, M, N, K):
+    rng = np.random.default_rng(M + N + K)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    got = orc.matmul(A, B)
+    want = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.abs(got - want).max() <= 1e-5 * max(1.0, np.abs(want).max()) * math.sqrt(K)
+
+
+def test_matmul_small_integers_exact(orc):
+    A = np.array([(i % 7) - 3.0 for i in range(12)], np.float32).reshape(4, 3)
+    B = np.array([(i % 5) * 0.5 for i in range(15)], np.float32).reshape(3, 5)
+    assert np.array_equal(orc.matmul(A, B), (A.astype(np.float64) @ B).astype(np.float32))
+
+
+def test_adam_closed_form(orc):
+    rng = np.random.default_rng(4)
+    p = rng.standard_normal(1000).astype(np.float32)
+    g = (rng.standard_normal(1000) * 1e-2).astype(np.float32)
+    q, m, v = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam_step(q, g, m, v, 1, 3e-4, 0.9, 0.999, 1e-8)
+    # first step: m_hat = g, v_hat = g^2 -> update lr*g/(|g|+eps) ~ lr*sign(g)
+    assert np.allclose(p - q, 3e-4 * np.sign(g), rtol=1e-3, atol=1e-9)
+    # AdamW with wd = 0 is Adam bit for bit
+    q2, m2, v2 = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam_step(q2, g, m2, v2, 1, 3e-4, 0.9, 0.999, 1e-8, wd=0.0)
+    assert np.array_equal(q.view(np.uint32), q2.view(np.uint32))
+    # with zero gradient only the decoupled decay acts: p <- p - lr*wd*p
+    q3, m3, v3 = p.copy(), np.zeros_like(p), np.zeros_like(p)
+    orc.adam_step(q3, np.zeros_like(p), m3, v3, 1, 3e-4, 0.9, 0.95, 1e-8, wd=0.1)
+    assert np.allclose(q3, p * (1 - 3e-4 * 0.1), rtol=1e-6)
+
+
+def test_sample_batch_windows(orc):
+    toks = orc.random_tokens(5000, 300, 1, 2)
+    ids, tgt = orc.sample_batch(toks, 50, 6, 9)
+    ids, tgt = ids.reshape(6, 50), tgt.reshape(6, 50)
+    assert np.array_equal(ids[:, 1:], tgt[:, :-1])
+    for w in range(6):
+        r = orc.pcg_stream(9 * 1000003 + w, 99 + w)
+        start = orc.lib().or_pcg_range_i64(C.byref(r), 0, 5000 - 50 - 1)
+        assert np.array_equal(ids[w], toks[start:start + 50])

@@ -69,7 +69,7 @@ static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
     hip_launch(g->k.rmsnorm_fwd, cdiv_u64(g->N, 4), 1, 1, 256, 1, 1, 0, args);
 }
 
-#define RMS_ROWS 32u
+#define RMS_ROWS 16u
 
 /* dx += RMSNorm backward; dw = sum over rows of dy*x*r  (gpu_train.c:132-140) */
 static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t rinv, hipDeviceptr_t dy,
@@ -81,10 +81,10 @@ static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
     hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
     i32 inb = (i32)nb, acc = 0;
     void* args2[] = { &part, &inb, &cols, &dw, &acc };
-    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 256), 1, 1, 256, 1, 1, 0, args2);
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
 }
 
-#define COLSUM_RPB 64u
+#define COLSUM_RPB 16u
 
 /* out[c] = sum_r in[r, c] (bias gradients; the role of colsum_acc,
  * gpu_train.c:120-123) */
@@ -93,10 +93,10 @@ static void colsum(GpuTrainer* g, hipDeviceptr_t in, hipDeviceptr_t out, i32 row
     i32 ld = cols, rpb = (i32)COLSUM_RPB;
     u32 nb = cdiv_u64((u64)rows, COLSUM_RPB);
     void* args[] = { &in, &rows, &cols, &ld, &rpb, &part };
-    hip_launch(g->k.colsum_partial, nb, cdiv_u64((u64)cols, 256), 1, 256, 1, 1, 0, args);
+    hip_launch(g->k.colsum_partial, nb, 1, 1, 256, 1, 1, 0, args);
     i32 inb = (i32)nb, acc = 0;
     void* args2[] = { &part, &inb, &cols, &out, &acc };
-    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 256), 1, 1, 256, 1, 1, 0, args2);
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
 }
 
 /* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
@@ -241,7 +241,6 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.attn_bwd_dkv = hip_get_kernel(c, name);
     snprintf(name, sizeof(name), "k_attn_bwd_dq_hd%u", g.hd);
     g.k.attn_bwd_dq = hip_get_kernel(c, name);
-    g.k.attn_bwd_prep = hip_get_kernel(c, "k_attn_bwd_prep");
 
     gpu_trainer_upload(&g, params, NULL_PTR);
     hip_sync();
@@ -374,7 +373,7 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
         ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
         {
             void* args[] = { &ap };
-            hip_launch(g->k.attn_fwd, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_fwd, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
         }
         /* x2 = x_in + (att @ Wo + bo) */
         gemm1(g, GEMM_NN, a->att, P_(g, pidx(l, PK_WO)), a->x2, N, D, D, D, D, D, 0.0f, P_(g, pidx(l, PK_BO)),
@@ -444,9 +443,8 @@ static void backward_pass(GpuTrainer* g) {
         ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
         {
             void* args[] = { &ap };
-            hip_launch(g->k.attn_bwd_prep, cdiv_u64((u64)g->N * g->H, 256), 1, 1, 256, 1, 1, 0, args);
-            hip_launch(g->k.attn_bwd_dkv, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
-            hip_launch(g->k.attn_bwd_dq, cdiv_u64(g->T, 128), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dq, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dkv, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
         }
         rope(g, g->dqkv, 1);
         gemm1(g, GEMM_TN, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), D, 3 * D, N, D, 3 * D, 3 * D, 0.0f, NULL,

@@ -76,7 +76,7 @@ k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w, float* _
 // train_kernels.cu:552-569).  The weight gradient dy*x*r is reduced over the
 // block's RMS_ROWS rows in row order and written as one partial row per
 // block; k_colsum_final adds the partials in block order.
-#define RMS_ROWS 32
+#define RMS_ROWS 16
 extern "C" __global__ void __launch_bounds__(256)
 k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ rinv,
               const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ wpart, int rows, int cols) {
@@ -85,7 +85,7 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
     const int r0 = blockIdx.x * RMS_ROWS;
     float* mine = part + wave * cols;
     for (int i = lane; i < cols; i += 64) mine[i] = 0.f;
-    // wave `wave` handles rows r0 + wave*8 .. +7, in order
+    // wave `wave` handles rows r0 + wave*RMS_ROWS/4 .. in order
     for (int rr = 0; rr < RMS_ROWS / 4; rr++) {
         int row = r0 + wave * (RMS_ROWS / 4) + rr;
         if (row >= rows) break;
@@ -114,28 +114,81 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
 }
 
 // ---------------------------------------------------------------- column sums
-// partial[b, c] = sum over rows [b*rpb, (b+1)*rpb) of in[r, c], rows in order.
+// Stage 1: partial[b, c] = sum of in[r, c] over the rpb rows of block b.
+// 256 threads = G row-lanes x C4 float4 column groups (G = 256 / C4 when a
+// row is narrower than 1024 floats): row-lane g adds rows g, g+G, ... in
+// order, then the G sums are added in g order through LDS.  Fixed
+// assignment and order, so the result is reproducible.
 extern "C" __global__ void __launch_bounds__(256)
 k_colsum_partial(const float* __restrict__ in, int rows, int cols, int ld, int rpb, float* __restrict__ partial) {
-    int b = blockIdx.x;
-    int c = blockIdx.y * 256 + threadIdx.x;
-    if (c >= cols) return;
-    int r = b * rpb, e = r + rpb;
-    if (e > rows) e = rows;
-    float s = 0.f;
-    for (; r < e; r++) s += in[(long long)r * ld + c];
-    partial[(long long)b * cols + c] = s;
+    __shared__ f32x4 red[256];
+    const int b = blockIdx.x, t = threadIdx.x;
+    const int r0 = b * rpb;
+    int r1 = r0 + rpb;
+    if (r1 > rows) r1 = rows;
+    if ((cols & 3) == 0 && (ld & 3) == 0) {
+        const int C4 = cols >> 2;
+        if (C4 >= 256) {
+            for (int c4 = t; c4 < C4; c4 += 256) {
+                f32x4 s = {0.f, 0.f, 0.f, 0.f};
+                for (int r = r0; r < r1; r++) s += *(const f32x4*)(in + (long long)r * ld + 4 * c4);
+                *(f32x4*)(partial + (long long)b * cols + 4 * c4) = s;
+            }
+            return;
+        }
+        const int G = 256 / C4;
+        const int c4 = t % C4, g = t / C4;
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+        if (g < G)
+            for (int r = r0 + g; r < r1; r += G) s += *(const f32x4*)(in + (long long)r * ld + 4 * c4);
+        red[t] = s;
+        __syncthreads();
+        if (t < C4) {
+            f32x4 acc = red[t];
+            for (int k = 1; k < G; k++) acc += red[k * C4 + t];
+            *(f32x4*)(partial + (long long)b * cols + 4 * t) = acc;
+        }
+        return;
+    }
+    for (int c = t; c < cols; c += 256) {
+        float s = 0.f;
+        for (int r = r0; r < r1; r++) s += in[(long long)r * ld + c];
+        partial[(long long)b * cols + c] = s;
+    }
 }
 
-// out[c] (+)= sum_b partial[b, c] in block order (bias / norm-weight grads,
-// the role of train_kernels.cu:518-531).
+// Stage 2: out[c] (+)= sum over b of partial[b, c].  A block covers 64
+// columns; its 4 wavefronts each add a contiguous quarter of the partial
+// rows in order, and the four quarter sums are added in order.  Loads are
+// issued 16 at a time ahead of their (ordered) additions.
 extern "C" __global__ void __launch_bounds__(256)
 k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __restrict__ out, int accumulate) {
-    int c = blockIdx.x * 256 + threadIdx.x;
-    if (c >= cols) return;
-    float s = partial[c];
-    for (int b = 1; b < nb; b++) s += partial[(long long)b * cols + c];
-    out[c] = accumulate ? out[c] + s : s;
+    __shared__ float red[4][64];
+    const int cl = threadIdx.x & 63, q = threadIdx.x >> 6;
+    const int c = blockIdx.x * 64 + cl;
+    const int per = (nb + 3) / 4;
+    const int b0 = q * per;
+    int b1 = b0 + per;
+    if (b1 > nb) b1 = nb;
+    float s = 0.f;
+    if (c < cols) {
+        const float* src = partial + c;
+        int b = b0;
+        for (; b + 16 <= b1; b += 16) {
+            float v[16];
+#pragma unroll
+            for (int k = 0; k < 16; k++) v[k] = src[(long long)(b + k) * cols];
+#pragma unroll
+            for (int k = 0; k < 16; k++) s += v[k];
+        }
+        for (; b < b1; b++) s += src[(long long)b * cols];
+    }
+    red[q][cl] = s;
+    __syncthreads();
+    if (q == 0 && c < cols) {
+        float v = ((red[0][cl] + red[1][cl]) + red[2][cl]) + red[3][cl];
+        out[c] = accumulate ? out[c] + v : v;
+    }
 }
 
 // ---------------------------------------------------------------- RoPE
@@ -213,11 +266,26 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     __shared__ float sm[4], ss[4];
     const long long row = blockIdx.x;
     float* z = logits + row * ld;
+    const bool vec = ((ld & 3) == 0);
     float m = -INFINITY, s = 0.f;
-    for (int j = threadIdx.x; j < V; j += 256) {
-        float v = z[j];
-        if (v > m) { s = s * expf(m - v) + 1.f; m = v; }
-        else s += expf(v - m);
+    if (vec) {
+        const int nq = (V + 3) >> 2;
+        for (int q = threadIdx.x; q < nq; q += 256) {
+            f32x4 v = ((const f32x4*)z)[q];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                if (4 * q + e >= V) break;
+                float x = v[e];
+                if (x > m) { s = s * expf(m - x) + 1.f; m = x; }
+                else s += expf(x - m);
+            }
+        }
+    } else {
+        for (int j = threadIdx.x; j < V; j += 256) {
+            float x = z[j];
+            if (x > m) { s = s * expf(m - x) + 1.f; m = x; }
+            else s += expf(x - m);
+        }
     }
     // wave-level fixed-order combine
 #pragma unroll
@@ -239,10 +307,25 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     if (threadIdx.x == 0) loss_rows[row] = (float)log((double)S) + M - zt;
     if (!write_grad) return;
     float inv = 1.0f / S;
-    for (int j = threadIdx.x; j < V; j += 256) {
-        float p = expf(z[j] - M) * inv;
-        if (j == (int)t) p -= 1.0f;
-        z[j] = p * grad_scale;
+    if (vec) {
+        const int nq = ld >> 2;
+        for (int q = threadIdx.x; q < nq; q += 256) {
+            f32x4 v = ((f32x4*)z)[q];
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                int j = 4 * q + e;
+                float p = (j < V) ? expf(v[e] - M) * inv : 0.f;
+                if (j == (int)t) p -= 1.0f;
+                v[e] = p * grad_scale;
+            }
+            ((f32x4*)z)[q] = v;
+        }
+    } else {
+        for (int j = threadIdx.x; j < V; j += 256) {
+            float p = expf(z[j] - M) * inv;
+            if (j == (int)t) p -= 1.0f;
+            z[j] = p * grad_scale;
+        }
     }
 }
 
