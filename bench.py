@@ -59,7 +59,7 @@ def load_trlm():
 class Sweep:
     """Device operands of the fifteen GEMMs and their launches."""
 
-    def __init__(self, trlm, dev):
+    def __init__(self, trlm, dev, M=M):
         self.dev = dev
         rng = np.random.default_rng(2026)
         self.items = []
@@ -217,6 +217,51 @@ def summarize_profile(path):
                                                           sum(v) / len(v) / 1e3, 100.0 * sum(v) / total))
 
 
+TILES = ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
+
+
+def tune(trlm, hip, reps, out_path=None):
+    """Time every aligned tile variant and split-K factor on the sweep GEMMs
+    (at M = B*T and at two smaller row counts) and print them, fastest
+    first; the automatic choice is marked '*'.  out_path: all timings as
+    JSON lines {name, M, N, K, layout, variant, splits, ms, tflops, auto}."""
+    dev = trlm.Device()
+    fh = open(out_path, "w") if out_path else None
+    for m_rows in (M, 2048, 512):
+        sweep = Sweep(trlm, dev, m_rows)
+        for it in sweep.items:
+            sweep.run(it)
+            auto = "%s/split%d" % dev.last_variant()
+            ta, tb, _, _, _, m, n, k = it[2][:8]
+            rows = []
+            for tile in TILES:
+                for sp in [1, 2, 3, 4, 6, 8, 12, 16, 24, 32]:
+                    if sp > 1 and k // sp < 256:
+                        continue
+                    dev.force(tile, sp)
+                    sweep.run(it)
+                    dev.sync()
+                    ms = time_events(hip, lambda: sweep.run(it), reps)
+                    name, got_sp = dev.last_variant()
+                    rows.append((it[1] / (ms * 1e-3) / 1e12, "%s/split%d" % (name, got_sp), ms))
+                    if fh:
+                        fh.write(json.dumps({"name": it[0], "M": m, "N": n, "K": k, "layout": [ta, tb],
+                                             "variant": name, "splits": got_sp, "ms": ms,
+                                             "tflops": rows[-1][0], "auto": rows[-1][1] == auto}) + "\n")
+            dev.force(None)
+            rows.sort(reverse=True)
+            print("%s M=%d  (auto %s)" % (it[0], m_rows, auto), flush=True)
+            for tf, name, ms in rows[:4]:
+                print("   %7.1f TF  %8.4f ms  %s%s" % (tf, ms, name, " *" if name == auto else ""), flush=True)
+            a = [r for r in rows if r[1] == auto]
+            if a and a[0] not in rows[:4]:
+                print("   %7.1f TF  %8.4f ms  %s *" % (a[0][0], a[0][2], auto), flush=True)
+        sweep.close()
+    if fh:
+        fh.close()
+    dev.close()
+
+
 def main():
     if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
         summarize_profile(sys.argv[2])
@@ -230,6 +275,9 @@ def main():
     ap.add_argument("--model-only", action="store_true",
                     help="only the B8 T1024 forward/train measurements (for focused profiling); "
                          "prints them as a JSON line without the sweep")
+    ap.add_argument("--tune", action="store_true",
+                    help="time every GEMM tile variant / split-K factor on the sweep shapes and exit")
+    ap.add_argument("--tune-out", default=None, help="with --tune: write every timing as JSON lines here")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
@@ -238,6 +286,9 @@ def main():
 
     trlm = load_trlm()
     _, hip = trlm.libs()
+    if args.tune:
+        tune(trlm, hip, max(3, args.steps // 2), args.tune_out)
+        return
     if args.model_only:
         print(json.dumps(model_benchmarks(trlm, args.steps, args.warmup)), flush=True)
         return

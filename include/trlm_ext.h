@@ -51,6 +51,15 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
                f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr);
 /* Name of the kernel variant and split-K factor the last trlm_gemm call used. */
 const char* trlm_gemm_last_variant(TrlmGemm* e, i32* splits);
+/* The variant and split-K factor trlm_gemm picks for 16-byte-aligned operands
+ * of this shape (host-only; no device call). */
+const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 batch, i32* splits);
+/* Tuning hook: make later calls on this engine use the named aligned tile
+ * variant ("256x128", "128x256", "128x128", "128x128_k32", "64x128",
+ * "64x128_k32", "64x64", "64x64_k32") and, when splits > 0, that split-K
+ * factor (single GEMMs only).  tile NULL restores automatic selection.
+ * Returns 0, or -1 for an unknown name (selection is then automatic). */
+i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits);
 
 /* Stream-event timing on the current context's stream. */
 typedef struct TrlmTimer { hipEvent_t start, stop; } TrlmTimer;

@@ -95,7 +95,7 @@ def test_undefined_symbols_are_runtime_only(trlm):
                "m_sqrtf"}
     other = {n for n in names if not (n.startswith("hip") or n.startswith("_") or n in runtime)}
     libc = {"fprintf", "fflush", "_exit", "fopen", "fseek", "ftell", "fread", "fclose", "malloc", "calloc",
-            "realloc", "free", "memset", "memcpy", "snprintf", "stderr", "stdout", "clock_gettime",
+            "realloc", "free", "memset", "memcpy", "strcmp", "snprintf", "stderr", "stdout", "clock_gettime",
             "pthread_mutex_lock", "pthread_mutex_unlock", "pthread_mutex_init", "pthread_mutex_destroy"}
     assert other <= libc, other - libc
     assert runtime & names == runtime, runtime - names
@@ -110,7 +110,8 @@ def test_code_object_has_every_kernel(trlm):
     names = set(re.findall(r'"(k_[a-z0-9_]+)"', src))
     names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
-    names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in ("128x128", "64x128", "64x64")}
+    names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in (
+        "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32")}
     names |= {"k_gemm_%s_64x64_u" % l for l in ("nn", "nt", "tn", "tt")}
     for n in sorted(names):
         assert n.encode() + b"\0" in blob, n
@@ -169,3 +170,30 @@ def test_sample_batch_bit_exact(trlm, orc, T, B, seed):
     hip.gpu_trainer_sample_batch(toks, len(toks), T, B, seed, ids, tgt)
     wi, wt = orc.sample_batch(toks, T, B, seed)
     assert np.array_equal(ids, wi) and np.array_equal(tgt, wt)
+
+
+def test_gemm_plan_is_a_pure_function_of_the_shape(trlm):
+    """The GEMM plan (variant, split-K) depends on (layout, M, N, K, batch)
+    only -- reruns of a shape take the same kernels, so results repeat bit for
+    bit -- and respects the split-K limits: single GEMMs only, every split at
+    least 256 deep, at most 32 splits."""
+    _, hip = trlm.libs()
+    sp = C.c_int32()
+    shapes = [(8192, 1152, 384), (8192, 384, 2048), (384, 1152, 8192), (8192, 31769, 384), (8192, 384, 31769),
+              (31769, 384, 8192), (1, 1, 1), (4, 5, 3), (512, 384, 1024), (100, 68, 4000), (64, 64, 0)]
+    for ta, tb in [(0, 0), (0, 1), (1, 0)]:
+        for M, N, K in shapes:
+            for batch in (1, 6):
+                first = hip.trlm_gemm_plan(ta, tb, M, N, K, batch, C.byref(sp)).decode(), sp.value
+                again = hip.trlm_gemm_plan(ta, tb, M, N, K, batch, C.byref(sp)).decode(), sp.value
+                assert first == again
+                name, splits = first
+                assert name.startswith("k_gemm_%s_" % ["nn", "nt", "tn"][ta * 2 + tb]), name
+                assert 1 <= splits <= 32
+                if splits > 1:
+                    assert batch == 1 and K // splits >= 224, (M, N, K, splits)
+    assert hip.trlm_gemm_plan(1, 1, 64, 64, 64, 1, C.byref(sp)) == b"k_gemm_tt_64x64_u" and sp.value == 1
+    # the LM-head forward (15,936 tiles of 128x128, 62 per CU) keeps the
+    # large tile and needs no split
+    name = hip.trlm_gemm_plan(0, 1, 8192, 31769, 384, 1, C.byref(sp)).decode()
+    assert name == "k_gemm_nt_128x128" and sp.value == 1

@@ -216,3 +216,30 @@ def test_gemm_lm_head_rows(dev):
     want = A[rows].astype(np.float64) @ E.T.astype(np.float64)
     ok, rel = close(got[rows], want)
     assert ok, rel
+
+
+TILES = ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_gemm_every_tile_variant(dev, tile, ta, tb):
+    """Each aligned tile variant, forced, on an off-grid shape (M, N not
+    tile multiples, K not a multiple of the k step) with the full epilogue,
+    then with a forced split-K; the selection is restored afterwards."""
+    rng = np.random.default_rng(len(tile) * 3 + ta + 2 * tb)
+    M, N, K = 300, 260, 1000
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    try:
+        for splits in (1, 3):
+            dev.force(tile, splits)
+            got, var = run_gemm(dev, A, B, ta, tb, alpha=0.5, beta=1.0, C0=C0, bias=bias, resid=resid)
+            assert var == ("k_gemm_%s_%s" % (["nn", "nt", "tn"][ta * 2 + tb], tile), splits), var
+            ok, rel = close(got, ref64(A, B, 0.5, 1.0, C0, bias, resid))
+            assert ok, (var, rel)
+    finally:
+        dev.force(None)

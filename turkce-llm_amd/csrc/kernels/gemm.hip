@@ -14,7 +14,7 @@
 //  - 256-thread workgroups = 4 wave64 in a 2x2 grid; each wave owns a
 //    (BM/2)x(BN/2) block of 32x32 MFMA accumulators.
 //  - Operands are staged through double-buffered LDS, one barrier per
-//    BK=16 step; the next global tile is prefetched into registers while the
+//    BK=16 (or 32) step; the next global tile is prefetched into registers while the
 //    current one feeds the matrix cores.
 //  - A K-contiguous operand is kept K-contiguous in LDS and read with one
 //    128-bit LDS read per 4 MFMA steps: lane l feeds k = kk+4*(l/32)+s at
@@ -40,8 +40,6 @@ struct GemmParams {
     int tiles_m, tiles_n;
 };
 
-#define GBK 16
-
 __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
     const int num = p.tiles_m * p.tiles_n;
     int bid = blockIdx.x;
@@ -61,24 +59,24 @@ __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, i
     tn = in / gm;
 }
 
-template <int R, bool KMAJOR>
+template <int R, int BK, bool KMAJOR>
 struct TileLds {
-    // KMAJOR: [R][GBK+4] (k contiguous); else [GBK][R] (m/n contiguous)
-    static constexpr int SIZE = KMAJOR ? R * (GBK + 4) : GBK * R;
+    // KMAJOR: [R][BK+4] (k contiguous); else [BK][R] (m/n contiguous)
+    static constexpr int SIZE = KMAJOR ? R * (BK + 4) : BK * R;
 };
 
-// Load one operand tile (R rows of m/n, GBK of k) from global memory into
+// Load one operand tile (R rows of m/n, BK of k) from global memory into
 // registers.  KMAJOR: element (r, k) at base[r*ld + k]; else base[k*ld + r].
-template <int R, bool KMAJOR, bool ALIGNED>
+template <int R, int BK, bool KMAJOR, bool ALIGNED>
 __device__ __forceinline__ void load_tile(const float* __restrict__ base, int ld, int r0, int rlim, int k0,
                                           int klim, f32x4* regs) {
-    constexpr int NL = R * GBK / 4 / 256;
+    constexpr int NL = R * BK / 4 / 256;
     const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         int idx = t + i * 256;
         int r, k;
-        if (KMAJOR) { r = idx >> 2; k = (idx & 3) * 4; }
+        if (KMAJOR) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
         else { k = idx / (R / 4); r = (idx % (R / 4)) * 4; }
         int gr = r0 + r, gk = k0 + k;
         f32x4 v = {0.f, 0.f, 0.f, 0.f};
@@ -107,16 +105,16 @@ __device__ __forceinline__ void load_tile(const float* __restrict__ base, int ld
     }
 }
 
-template <int R, bool KMAJOR>
+template <int R, int BK, bool KMAJOR>
 __device__ __forceinline__ void store_tile(float* lds, const f32x4* regs) {
-    constexpr int NL = R * GBK / 4 / 256;
+    constexpr int NL = R * BK / 4 / 256;
     const int t = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NL; i++) {
         int idx = t + i * 256;
         if (KMAJOR) {
-            int r = idx >> 2, k = (idx & 3) * 4;
-            *(f32x4*)(lds + r * (GBK + 4) + k) = regs[i];
+            int r = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
+            *(f32x4*)(lds + r * (BK + 4) + k) = regs[i];
         } else {
             int k = idx / (R / 4), r = (idx % (R / 4)) * 4;
             *(f32x4*)(lds + k * R + r) = regs[i];
@@ -125,12 +123,12 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4* regs) {
 }
 
 // Operand values of one 32-row MFMA block for the 4 steps of an 8-k chunk.
-template <int R, bool KMAJOR>
+template <int R, int BK, bool KMAJOR>
 __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, int lane) {
     const int row = rb + (lane & 31);
     const int kq = kk + 4 * (lane >> 5);
     if (KMAJOR) {
-        return *(const f32x4*)(lds + row * (GBK + 4) + kq);
+        return *(const f32x4*)(lds + row * (BK + 4) + kq);
     } else {
         f32x4 v;
 #pragma unroll
@@ -139,14 +137,14 @@ __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, in
     }
 }
 
-template <int TA, int TB, int BM, int BN, bool ALIGNED>
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
 __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
-    constexpr int ASZ = TileLds<BM, AK>::SIZE, BSZ = TileLds<BN, BK_>::SIZE;
-    constexpr int NLA = BM * GBK / 4 / 256, NLB = BN * GBK / 4 / 256;
+    constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
+    constexpr int NLA = BM * BK / 4 / 256, NLB = BN * BK / 4 / 256;
     __shared__ __attribute__((aligned(16))) float lds[2 * (ASZ + BSZ)];
 
     int tm, tn;
@@ -174,17 +172,17 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
 
     f32x4 ra[NLA > 0 ? NLA : 1], rb[NLB > 0 ? NLB : 1];
     auto gload = [&](int k0) {
-        if (AK) load_tile<BM, true, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
-        else load_tile<BM, false, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
-        if (BK_) load_tile<BN, true, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
-        else load_tile<BN, false, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+        if (AK) load_tile<BM, BK, true, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+        else load_tile<BM, BK, false, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+        if (BK_) load_tile<BN, BK, true, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+        else load_tile<BN, BK, false, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
     };
     auto lstore = [&](int buf) {
-        store_tile<BM, AK>(lds + buf * (ASZ + BSZ), ra);
-        store_tile<BN, BK_>(lds + buf * (ASZ + BSZ) + ASZ, rb);
+        store_tile<BM, BK, AK>(lds + buf * (ASZ + BSZ), ra);
+        store_tile<BN, BK, BK_>(lds + buf * (ASZ + BSZ) + ASZ, rb);
     };
 
-    const int nk = (ke - kb + GBK - 1) / GBK;
+    const int nk = (ke - kb + BK - 1) / BK;
     if (nk > 0) {
         gload(kb);
         lstore(0);
@@ -192,16 +190,16 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     __syncthreads();
     for (int kt = 0; kt < nk; kt++) {
         const int cur = kt & 1;
-        if (kt + 1 < nk) gload(kb + (kt + 1) * GBK);
+        if (kt + 1 < nk) gload(kb + (kt + 1) * BK);
         const float* la = lds + cur * (ASZ + BSZ);
         const float* lb = la + ASZ;
 #pragma unroll
-        for (int kk = 0; kk < GBK; kk += 8) {
+        for (int kk = 0; kk < BK; kk += 8) {
             f32x4 fa[FM], fb[FN];
 #pragma unroll
-            for (int i = 0; i < FM; i++) fa[i] = fetch_frag<BM, AK>(la, wm0 + i * 32, kk, lane);
+            for (int i = 0; i < FM; i++) fa[i] = fetch_frag<BM, BK, AK>(la, wm0 + i * 32, kk, lane);
 #pragma unroll
-            for (int j = 0; j < FN; j++) fb[j] = fetch_frag<BN, BK_>(lb, wn0 + j * 32, kk, lane);
+            for (int j = 0; j < FN; j++) fb[j] = fetch_frag<BN, BK, BK_>(lb, wn0 + j * 32, kk, lane);
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -238,25 +236,34 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
         }
 }
 
-#define GEMM_KERNEL(NAME, TA, TB, BM, BN, AL)                                           \
-    extern "C" __global__ void __launch_bounds__(256) NAME(GemmParams p) {             \
-        gemm_body<TA, TB, BM, BN, AL>(p);                                              \
+#define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE)                                 \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) \
+    NAME(GemmParams p) {                                                                 \
+        gemm_body<TA, TB, BM, BN, BK, AL>(p);                                            \
     }
 
-// name: k_gemm_<layout>_<BM>x<BN>[_u]  (_u = unaligned operands, scalar loads)
-GEMM_KERNEL(k_gemm_nn_128x128, 0, 0, 128, 128, true)
-GEMM_KERNEL(k_gemm_nn_64x128, 0, 0, 64, 128, true)
-GEMM_KERNEL(k_gemm_nn_64x64, 0, 0, 64, 64, true)
-GEMM_KERNEL(k_gemm_nt_128x128, 0, 1, 128, 128, true)
-GEMM_KERNEL(k_gemm_nt_64x128, 0, 1, 64, 128, true)
-GEMM_KERNEL(k_gemm_nt_64x64, 0, 1, 64, 64, true)
-GEMM_KERNEL(k_gemm_tn_128x128, 1, 0, 128, 128, true)
-GEMM_KERNEL(k_gemm_tn_64x128, 1, 0, 64, 128, true)
-GEMM_KERNEL(k_gemm_tn_64x64, 1, 0, 64, 64, true)
-GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, false)
-GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, false)
-GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, false)
-GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, false)
+#define GEMM_LAYOUTS(TILE, BM, BN, BK, WPE)                                             \
+    GEMM_KERNEL(k_gemm_nn_##TILE, 0, 0, BM, BN, BK, true, WPE)                          \
+    GEMM_KERNEL(k_gemm_nt_##TILE, 0, 1, BM, BN, BK, true, WPE)                          \
+    GEMM_KERNEL(k_gemm_tn_##TILE, 1, 0, BM, BN, BK, true, WPE)
+
+// name: k_gemm_<layout>_<BM>x<BN>[_k32][_u]
+//   _k32: 32-deep k step (one barrier per 32 k instead of 16)
+//   _u:   unaligned operands (scalar loads), 16-deep k step
+// Waves own (BM/2)x(BN/2): 256x128 / 128x256 tiles hold 8 accumulator blocks
+// per wave and are held to 2 waves per SIMD (<= 128 VGPRs + 128 AGPRs).
+GEMM_LAYOUTS(256x128, 256, 128, 16, 2)
+GEMM_LAYOUTS(128x256, 128, 256, 16, 2)
+GEMM_LAYOUTS(128x128, 128, 128, 16, 1)
+GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 1)
+GEMM_LAYOUTS(64x128, 64, 128, 16, 1)
+GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 1)
+GEMM_LAYOUTS(64x64, 64, 64, 16, 1)
+GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 1)
+GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1)
+GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1)
+GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, 16, false, 1)
+GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, 16, false, 1)
 
 // out[m,n] = alpha * sum_s W[s][m,n] (+ beta*out) (+ bias[n]); out = resid + v.
 // Partials are summed in split order, so the result is reproducible.

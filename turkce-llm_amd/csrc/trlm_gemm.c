@@ -4,12 +4,14 @@
  * helpers (model/gpu_train.c:42-118): same operand conventions (NN, NT, TN;
  * batched with element strides; alpha/beta; bias and residual epilogue),
  * with the tile shape and split-K chosen per problem for 256 CUs:
- *   - 128x128 tiles when that gives >= 2 workgroups per CU,
- *     else 64x128, else 64x64;
- *   - split-K for single GEMMs with a large K and too few tiles (the
- *     weight-gradient TN forms, K = B*T; dX with K = vocab): splits write
- *     raw partials to a workspace that k_gemm_splitk_reduce sums in split
- *     order, so the result stays deterministic (no atomics);
+ *   - (tile, split-K) minimise a load-balance cost model (select_plan): the
+ *     busiest CU's share of workgroups, the variant's residency and
+ *     efficiency, and the split partials' HBM round trip.  The plan depends
+ *     on (M, N, K, batch) only, so reruns are bit-identical;
+ *   - split-K (single GEMMs: weight gradients with K = B*T, dX with
+ *     K = vocab, short-M shapes): splits write raw partials to a workspace
+ *     that k_gemm_splitk_reduce sums in split order, so the result stays
+ *     deterministic (no atomics);
  *   - operands whose rows are not 16-byte aligned go to the _u variants,
  *     which use scalar loads.
  */
@@ -37,33 +39,41 @@ typedef struct GemmParams {
 } GemmParams;
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
-enum { T_128x128 = 0, T_64x128 = 1, T_64x64 = 2 };
-static const int TILE_BM[3] = { 128, 64, 64 };
-static const int TILE_BN[3] = { 128, 128, 64 };
 static const char* LAYOUT_NAME[4] = { "nn", "nt", "tn", "tt" };
-static const char* TILE_NAME[3] = { "128x128", "64x128", "64x64" };
+
+/* Aligned tile variants (gemm.hip): name suffix, tile rows/cols, k step. */
+typedef struct TileDef { const char* name; int bm, bn, bk; } TileDef;
+enum { T_256x128, T_128x256, T_128x128, T_128x128_K32, T_64x128, T_64x128_K32, T_64x64, T_64x64_K32, T_COUNT };
+static const TileDef TILES[T_COUNT] = {
+    { "256x128", 256, 128, 16 }, { "128x256", 128, 256, 16 }, { "128x128", 128, 128, 16 },
+    { "128x128_k32", 128, 128, 32 }, { "64x128", 64, 128, 16 }, { "64x128_k32", 64, 128, 32 },
+    { "64x64", 64, 64, 16 }, { "64x64_k32", 64, 64, 32 },
+};
 
 #define CUS 256
-#define GBK 16
+#define KCHUNK_ALIGN 32  /* split-K chunks are multiples of every variant's k step */
 
 struct TrlmGemm {
     HipCtx* ctx;
-    hipFunction_t k[3][3];
+    hipFunction_t k[3][T_COUNT];
     hipFunction_t ku[4];
     hipFunction_t reduce;
     hipDeviceptr_t ws;
     u64 ws_floats;
     char last[48];
     i32 last_splits;
+    i32 force_tile;    /* -1: automatic selection */
+    i32 force_splits;  /* 0: automatic split-K */
 };
 
 TrlmGemm* trlm_gemm_create(HipCtx* ctx) {
     TrlmGemm* e = (TrlmGemm*)calloc(1, sizeof(TrlmGemm));
     e->ctx = ctx;
+    e->force_tile = -1;
     char name[64];
     for (int l = 0; l < 3; l++)
-        for (int t = 0; t < 3; t++) {
-            snprintf(name, sizeof(name), "k_gemm_%s_%s", LAYOUT_NAME[l], TILE_NAME[t]);
+        for (int t = 0; t < T_COUNT; t++) {
+            snprintf(name, sizeof(name), "k_gemm_%s_%s", LAYOUT_NAME[l], TILES[t].name);
             e->k[l][t] = hip_get_kernel(ctx, name);
         }
     for (int l = 0; l < 4; l++) {
@@ -85,6 +95,18 @@ const char* trlm_gemm_last_variant(TrlmGemm* e, i32* splits) {
     return e->last;
 }
 
+i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits) {
+    e->force_tile = -1;
+    e->force_splits = splits > 0 ? splits : 0;
+    if (!tile || !tile[0]) return 0;
+    for (int t = 0; t < T_COUNT; t++)
+        if (strcmp(tile, TILES[t].name) == 0) {
+            e->force_tile = t;
+            return 0;
+        }
+    return -1;
+}
+
 static int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
@@ -92,6 +114,87 @@ static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 static void launch(hipFunction_t f, GemmParams* p, u32 gz) {
     void* args[] = { p };
     hip_launch(f, (u32)(p->tiles_m * p->tiles_n), 1, gz, 256, 1, 1, 0, args);
+}
+
+static long long tiles_of(int t, int M, int N, u32 batch) {
+    return (long long)cdiv(M, TILES[t].bm) * cdiv(N, TILES[t].bn) * batch;
+}
+
+/* Split-K factor for a single GEMM with few output tiles and a long K:
+ * enough splits for ~2 workgroups per CU, each split >= 256 deep.  Used
+ * when a tile is forced without a split factor. */
+static int auto_splits(long long tiles, int K) {
+    if (K < 512 || tiles >= CUS) return 1;
+    int s = cdiv(2 * CUS, tiles);
+    if (s > K / 256) s = K / 256;
+    if (s > 32) s = 32;
+    return s < 1 ? 1 : s;
+}
+
+/* Plan model: the tiles' workgroups are spread evenly over the 256 CUs, so
+ * the busiest CU runs n = ceil(workgroups / 256) of them, `occ` at a time
+ * (the variant's resident workgroups per CU).  A CU with c resident
+ * workgroups runs at CU_RATE(c) of its steady-state rate (one resident
+ * 4-wave workgroup cannot hide its own load latency), and each variant has
+ * its own steady-state efficiency.  Split-K adds the partials' round trip
+ * through HBM plus the reduction launch.  Constants fitted to MI355X
+ * timings of every variant/split on the model's GEMMs at 512-8192 rows. */
+typedef struct PlanTile { int tile; int occ; double eff; } PlanTile;
+static const PlanTile PLAN_TILES[] = {
+    { T_128x128, 3, 1.02 }, { T_128x256, 2, 1.01 }, { T_256x128, 2, 0.91 },
+    { T_64x128_K32, 2, 0.93 }, { T_64x64_K32, 4, 0.98 },
+};
+static const int PLAN_SPLITS[] = { 1, 2, 3, 4, 6, 8, 12, 16, 24, 32 };
+#define PLAN_CU_FLOPS 0.6e12     /* per-CU steady-state fp32 MFMA rate, FLOP/s */
+#define PLAN_SPLIT_BW 10.7e12    /* effective bytes/s of the partials' round trip */
+#define PLAN_SPLIT_FIXED 2.5e-6  /* reduction launch, s */
+
+static double cu_rate(int c) { return c <= 1 ? 0.67 : (c == 2 ? 0.97 : 1.0); }
+
+static double plan_cost(const PlanTile* pt, int M, int N, int K, u32 batch, int splits) {
+    const TileDef* td = &TILES[pt->tile];
+    double wg = (double)cdiv(M, td->bm) * cdiv(N, td->bn) * batch * splits;
+    int kch = splits > 1 ? cdiv(cdiv(K, splits), KCHUNK_ALIGN) * KCHUNK_ALIGN : K;
+    long long n = (long long)((wg + CUS - 1) / CUS);
+    double w = 2.0 * td->bm * td->bn * (double)kch / (pt->eff * PLAN_CU_FLOPS);
+    long long full = n / pt->occ, rest = n % pt->occ;
+    double t = (double)full * pt->occ * w / cu_rate(pt->occ);
+    if (rest) t += (double)rest * w / cu_rate((int)rest);
+    if (splits > 1) t += (splits + 1) * (double)M * N * 4.0 / PLAN_SPLIT_BW + PLAN_SPLIT_FIXED;
+    return t;
+}
+
+static void select_plan(int M, int N, int K, u32 batch, int* tile, int* splits) {
+    double best = 0.0;
+    *tile = T_128x128;
+    *splits = 1;
+    for (size_t i = 0; i < sizeof(PLAN_TILES) / sizeof(PLAN_TILES[0]); i++)
+        for (size_t j = 0; j < sizeof(PLAN_SPLITS) / sizeof(PLAN_SPLITS[0]); j++) {
+            int sp = PLAN_SPLITS[j];
+            if (sp > 1 && (batch != 1 || K / sp < 256)) continue;
+            double c = plan_cost(&PLAN_TILES[i], M, N, K, batch, sp);
+            if ((i == 0 && j == 0) || c < best) {
+                best = c;
+                *tile = PLAN_TILES[i].tile;
+                *splits = sp;
+            }
+        }
+}
+
+const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 batch, i32* splits) {
+    static __thread char name[48];
+    int layout = trans_a ? (trans_b ? 3 : L_TN) : (trans_b ? L_NT : L_NN);
+    int tile, sp;
+    if (layout == 3) {
+        snprintf(name, sizeof(name), "k_gemm_tt_64x64_u");
+        sp = 1;
+    } else {
+        select_plan(M, N, K, batch ? batch : 1, &tile, &sp);
+        if (sp > 1) sp = cdiv(K, cdiv(cdiv(K, sp), KCHUNK_ALIGN) * KCHUNK_ALIGN);
+        snprintf(name, sizeof(name), "k_gemm_%s_%s", LAYOUT_NAME[layout], TILES[tile].name);
+    }
+    if (splits) *splits = sp;
+    return name;
 }
 
 void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
@@ -123,31 +226,22 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
         return;
     }
 
-    long long t128 = (long long)cdiv(M, 128) * cdiv(N, 128) * batch;
-    long long t64x128 = (long long)cdiv(M, 64) * cdiv(N, 128) * batch;
-    int tile;
-    int splits = 1;
-    if (batch == 1 && K >= 512 && t128 < CUS) {
-        /* few output tiles, long K: split K across workgroups */
-        tile = T_128x128;
-        splits = cdiv(2 * CUS, t128);
-        if (splits > K / 256) splits = K / 256;
-        if (splits > 32) splits = 32;
-        if (splits < 1) splits = 1;
-    } else if (t128 >= 2 * CUS) {
-        tile = T_128x128;
-    } else if (t64x128 >= 2 * CUS) {
-        tile = T_64x128;
-    } else {
-        tile = T_64x64;
+    int tile, splits;
+    select_plan(M, N, K, batch, &tile, &splits);
+    if (e->force_tile >= 0) {
+        tile = e->force_tile;
+        splits = batch == 1 ? auto_splits(tiles_of(tile, M, N, 1), K) : 1;
     }
-    p.tiles_m = cdiv(M, TILE_BM[tile]);
-    p.tiles_n = cdiv(N, TILE_BN[tile]);
+    if (e->force_splits > 0 && batch == 1) splits = e->force_splits;
+    p.tiles_m = cdiv(M, TILES[tile].bm);
+    p.tiles_n = cdiv(N, TILES[tile].bn);
+    int kchunk = K;
+    if (splits > 1 && K < 2 * KCHUNK_ALIGN) splits = 1;
     if (splits > 1) {
-        int kchunk = cdiv(cdiv(K, splits), GBK) * GBK;
+        kchunk = cdiv(cdiv(K, splits), KCHUNK_ALIGN) * KCHUNK_ALIGN;
         splits = cdiv(K, kchunk);
     }
-    snprintf(e->last, sizeof(e->last), "k_gemm_%s_%s", LAYOUT_NAME[layout], TILE_NAME[tile]);
+    snprintf(e->last, sizeof(e->last), "k_gemm_%s_%s", LAYOUT_NAME[layout], TILES[tile].name);
     e->last_splits = splits;
     if (splits <= 1) {
         launch(e->k[layout][tile], &p, batch);
@@ -164,7 +258,7 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
     q.C = (float*)e->ws;
     q.ldc = N;
     q.sW = (long long)M * N;
-    q.kchunk = cdiv(cdiv(K, splits), GBK) * GBK;
+    q.kchunk = kchunk;
     q.splits = splits;
     q.alpha = 1.0f; q.beta = 0.0f; q.bias = NULL; q.resid = NULL;
     launch(e->k[layout][tile], &q, (u32)splits);

@@ -184,6 +184,9 @@ def _bind(host, hip):
                                   C.c_uint32, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_float,
                                   C.c_void_p, C.c_void_p, C.c_int32])
     _sig(hip, "trlm_gemm_last_variant", C.c_char_p, [C.c_void_p, C.POINTER(C.c_int32)])
+    _sig(hip, "trlm_gemm_plan", C.c_char_p, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_uint32,
+                                             C.POINTER(C.c_int32)])
+    _sig(hip, "trlm_gemm_force", C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32])
     TP = C.POINTER(TrlmTimer)
     _sig(hip, "trlm_timer_create", None, [TP])
     _sig(hip, "trlm_timer_destroy", None, [TP])
@@ -428,6 +431,12 @@ class Device:
         sp = C.c_int32(0)
         name = self.hip.trlm_gemm_last_variant(self.gemm, C.byref(sp))
         return name.decode(), sp.value
+
+    def force(self, tile=None, splits=0):
+        """Pin later GEMMs on this device to one tile variant / split-K factor
+        (None restores automatic selection)."""
+        if self.hip.trlm_gemm_force(self.gemm, tile.encode() if tile else None, splits) != 0:
+            raise ValueError("unknown GEMM tile variant %r" % tile)
 
     def sync(self):
         self.hip.hip_sync()
