@@ -137,45 +137,61 @@ __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, in
     }
 }
 
-template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
-__device__ __forceinline__ void gemm_body(const GemmParams& p) {
+// Interior-tile loads: every element of the R x BK tile is in bounds, so
+// each thread streams f32x4s through fixed row pointers with no checks.
+template <int R, int BK, bool KMAJOR>
+struct TileStream {
+    static constexpr int NL = R * BK / 4 / 256;
+    const float* ptr[NL];
+    long long step;
+    __device__ __forceinline__ void init(const float* __restrict__ base, int ld, int r0, int k0) {
+        const int t = threadIdx.x;
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            int idx = t + i * 256;
+            int r, k;
+            if (KMAJOR) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
+            else { k = idx / (R / 4); r = (idx % (R / 4)) * 4; }
+            ptr[i] = KMAJOR ? base + (long long)(r0 + r) * ld + (k0 + k) : base + (long long)(k0 + k) * ld + (r0 + r);
+        }
+        step = KMAJOR ? BK : (long long)BK * ld;
+    }
+    __device__ __forceinline__ void load(f32x4* regs) {
+#pragma unroll
+        for (int i = 0; i < NL; i++) {
+            regs[i] = *(const f32x4*)ptr[i];
+            ptr[i] += step;
+        }
+    }
+};
+
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED, bool FULL>
+__device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* A, const float* B, int m0, int n0,
+                                              int kb, int ke, float* lds, f32x16 (&acc)[BM / 64][BN / 64]) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
     constexpr int WM = BM / 2, WN = BN / 2;
     constexpr int FM = WM / 32, FN = WN / 32;
     constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
     constexpr int NLA = BM * BK / 4 / 256, NLB = BN * BK / 4 / 256;
-    __shared__ __attribute__((aligned(16))) float lds[2 * (ASZ + BSZ)];
-
-    int tm, tn;
-    gemm_tile_coords(p, tm, tn);
-    const int z = blockIdx.z;
-    const int batch = z / p.splits, split = z - batch * p.splits;
-    const float* A = p.A + batch * p.sA;
-    const float* B = p.B + batch * p.sB;
-    float* C = p.C + batch * p.sC + split * p.sW;
-    const int m0 = tm * BM, n0 = tn * BN;
-    const int kb = split * p.kchunk;
-    int ke = kb + p.kchunk;
-    if (ke > p.K) ke = p.K;
-
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
 
-    f32x16 acc[FM][FN];
-#pragma unroll
-    for (int i = 0; i < FM; i++)
-#pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
-
     f32x4 ra[NLA > 0 ? NLA : 1], rb[NLB > 0 ? NLB : 1];
+    TileStream<BM, BK, AK> sa;
+    TileStream<BN, BK, BK_> sb;
+    if (FULL) {
+        sa.init(A, p.lda, m0, kb);
+        sb.init(B, p.ldb, n0, kb);
+    }
     auto gload = [&](int k0) {
-        if (AK) load_tile<BM, BK, true, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
-        else load_tile<BM, BK, false, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
-        if (BK_) load_tile<BN, BK, true, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
-        else load_tile<BN, BK, false, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+        if (FULL) {
+            sa.load(ra);
+            sb.load(rb);
+        } else {
+            load_tile<BM, BK, AK, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+            load_tile<BN, BK, BK_, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
+        }
     };
     auto lstore = [&](int buf) {
         store_tile<BM, BK, AK>(lds + buf * (ASZ + BSZ), ra);
@@ -211,6 +227,45 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
         if (kt + 1 < nk) lstore(cur ^ 1);
         __syncthreads();
     }
+}
+
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
+__device__ __forceinline__ void gemm_body(const GemmParams& p) {
+    constexpr bool AK = (TA == 0);   // A K-contiguous
+    constexpr bool BK_ = (TB == 1);  // B K-contiguous
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
+    __shared__ __attribute__((aligned(16))) float lds[2 * (ASZ + BSZ)];
+
+    int tm, tn;
+    gemm_tile_coords(p, tm, tn);
+    const int z = blockIdx.z;
+    const int batch = z / p.splits, split = z - batch * p.splits;
+    const float* A = p.A + batch * p.sA;
+    const float* B = p.B + batch * p.sB;
+    float* C = p.C + batch * p.sC + split * p.sW;
+    const int m0 = tm * BM, n0 = tn * BN;
+    const int kb = split * p.kchunk;
+    int ke = kb + p.kchunk;
+    if (ke > p.K) ke = p.K;
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+    f32x16 acc[FM][FN];
+#pragma unroll
+    for (int i = 0; i < FM; i++)
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
+
+    // Interior tiles whose k-range is whole BK steps take the check-free
+    // loop; edge tiles (and the scalar-load variants) the guarded one.
+    const bool full = ALIGNED && m0 + BM <= p.M && n0 + BN <= p.N && ke > kb && (ke - kb) % BK == 0;
+    if (full) gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, ALIGNED>(p, A, B, m0, n0, kb, ke, lds, acc);
+    else gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, false>(p, A, B, m0, n0, kb, ke, lds, acc);
 
     // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.
     const int half = lane >> 5, col_l = lane & 31;
