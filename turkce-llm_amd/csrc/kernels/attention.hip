@@ -46,21 +46,39 @@ struct AttnParams {
     float scale;       // 1/sqrt(HD)
 };
 
-// Cooperative load of one [64 x HD] tile (rows r0.., columns col0.., row
-// stride ld; rows >= rlim read as 0) into LDS with row stride HD+4, by all
-// 256 threads.
+// One [64 x HD] tile (rows r0.., columns col0.., row stride ld) held in
+// registers across the 256 threads of a workgroup: thread t holds the
+// f32x4 at row (t + 256 i) / (HD/4), column 4 ((t + 256 i) % (HD/4)).
+// Loading and storing are separate steps so that all of a stage's loads are
+// in flight together (and can be issued one stage ahead of the LDS store).
 template <int HD>
-__device__ __forceinline__ void att_tile(float* lds, const float* base, int ld, int r0, int rlim, int col0) {
-    constexpr int NQ = 64 * HD / 4 / 256;
+struct AttTile {
+    static constexpr int NQ = 64 * HD / 4 / 256;
+    f32x4 v[NQ];
+    // rows >= rlim read as 0 (their address is clamped to row rlim-1, so
+    // every load stays inside the tensor)
+    __device__ __forceinline__ void load(const float* base, int ld, int r0, int rlim, int col0) {
 #pragma unroll
-    for (int i = 0; i < NQ; i++) {
-        int idx = threadIdx.x + i * 256;
-        int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
-        f32x4 v = {0.f, 0.f, 0.f, 0.f};
-        if (r0 + r < rlim) v = *(const f32x4*)(base + (long long)(r0 + r) * ld + col0 + c);
-        *(f32x4*)(lds + r * (HD + 4) + c) = v;
+        for (int i = 0; i < NQ; i++) {
+            int idx = threadIdx.x + i * 256;
+            int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
+            int row = r0 + r;
+            bool ok = row < rlim;
+            f32x4 x = *(const f32x4*)(base + (long long)(ok ? row : rlim - 1) * ld + col0 + c);
+            if (!ok) x = f32x4{0.f, 0.f, 0.f, 0.f};
+            v[i] = x;
+        }
     }
-}
+    // LDS layout [64][HD + 4]
+    __device__ __forceinline__ void store(float* lds) const {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            int idx = threadIdx.x + i * 256;
+            int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
+            *(f32x4*)(lds + r * (HD + 4) + c) = v[i];
+        }
+    }
+};
 
 // Row-fragment of 32 rows for the d-steps of chunk j: lane l gets
 // X[rb + l%32][8j + 4*(l/32) + s], s = 0..3.
@@ -135,17 +153,31 @@ __device__ void flash_fwd(const AttnParams& p) {
     const int niter = (nkv + 1) / 2;
     const float* Ks = lds + part * 2 * 64 * LD;
     const float* Vs = Ks + 64 * LD;
-    for (int it = 0; it < niter; it++) {
-        __syncthreads();
+    // K and V of the stage's two key blocks go through registers, fetched one
+    // stage ahead so that their loads overlap the previous stage's MFMAs.
+    AttTile<HD> tk[2], tv[2];
+    auto fetch = [&](int it) {
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const int kb = 2 * it + pp;
             if (kb < nkv) {
-                att_tile<HD>(lds + pp * 2 * 64 * LD, qkv, p.ldq, kb * 64, p.T, kcol);
-                att_tile<HD>(lds + pp * 2 * 64 * LD + 64 * LD, qkv, p.ldq, kb * 64, p.T, vcol);
+                tk[pp].load(qkv, p.ldq, kb * 64, p.T, kcol);
+                tv[pp].load(qkv, p.ldq, kb * 64, p.T, vcol);
+            }
+        }
+    };
+    fetch(0);
+    for (int it = 0; it < niter; it++) {
+        __syncthreads();
+#pragma unroll
+        for (int pp = 0; pp < 2; pp++) {
+            if (2 * it + pp < nkv) {
+                tk[pp].store(lds + pp * 2 * 64 * LD);
+                tv[pp].store(lds + pp * 2 * 64 * LD + 64 * LD);
             }
         }
         __syncthreads();
+        if (it + 1 < niter) fetch(it + 1);
         const int kb = 2 * it + part;
         const int kv0 = kb * 64;
         if (kb >= nkv || kv0 > qw0 + 31) continue;
@@ -288,13 +320,21 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
     const float* Ks = lds + part * 2 * 64 * LD;
     const float* Vs = Ks + 64 * LD;
     for (int it = 0; it < niter; it++) {
-        __syncthreads();
+        // K, V of each of the stage's two key blocks: all loads of a block
+        // are in flight together, then stored (registers are too scarce
+        // here to fetch a whole stage ahead)
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
-            const int kb = 2 * it + pp;
-            if (kb < nkv) {
-                att_tile<HD>(lds + pp * 2 * 64 * LD, qkv, p.ldq, kb * 64, p.T, kcol);
-                att_tile<HD>(lds + pp * 2 * 64 * LD + 64 * LD, qkv, p.ldq, kb * 64, p.T, vcol);
+            const int kbp = 2 * it + pp;
+            AttTile<HD> tk, tv;
+            if (kbp < nkv) {
+                tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
+                tv.load(qkv, p.ldq, kbp * 64, p.T, vcol);
+            }
+            if (pp == 0) __syncthreads();
+            if (kbp < nkv) {
+                tk.store(lds + pp * 2 * 64 * LD);
+                tv.store(lds + pp * 2 * 64 * LD + 64 * LD);
             }
         }
         __syncthreads();
@@ -397,19 +437,32 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     const float* Ls = Gs + 64 * LD;
     const float* Ds = Ls + 64;
     for (int it = 0; it < niter; it++) {
-        __syncthreads();
+        // Q, dO (+ L, D) of the stage's two query blocks, one tile at a time:
+        // a tile's loads are in flight together, then stored (the K, V
+        // operands and four accumulators leave room for one tile only)
 #pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            const int j = 2 * it + pp;
-            if (j < nblk) {
-                const int q0 = (kb + j) * 64;
+        for (int tt = 0; tt < 4; tt++) {
+            const int pp = tt >> 1, jp = 2 * it + pp;
+            const bool isq = (tt & 1) == 0;
+            AttTile<HD> tl;
+            float lv = 0.f, dd = 0.f;
+            const int q0 = (kb + jp) * 64;
+            if (jp < nblk) {
+                if (isq) tl.load(qkv, p.ldq, q0, p.T, qcol);
+                else tl.load(dO, p.ldo, q0, p.T, qcol);
+                const int q = q0 + (threadIdx.x & 63);
+                if (isq && threadIdx.x < 64 && q < p.T) {
+                    lv = lse[q];
+                    dd = dv[q];
+                }
+            }
+            if (tt == 0) __syncthreads();
+            if (jp < nblk) {
                 float* base = lds + pp * TILE;
-                att_tile<HD>(base, qkv, p.ldq, q0, p.T, qcol);
-                att_tile<HD>(base + 64 * LD, dO, p.ldo, q0, p.T, qcol);
-                if (threadIdx.x < 64) {
-                    const int q = q0 + threadIdx.x;
-                    base[2 * 64 * LD + threadIdx.x] = (q < p.T) ? lse[q] : 0.f;
-                    base[2 * 64 * LD + 64 + threadIdx.x] = (q < p.T) ? dv[q] : 0.f;
+                tl.store(base + (isq ? 0 : 64 * LD));
+                if (isq && threadIdx.x < 64) {
+                    base[2 * 64 * LD + threadIdx.x] = lv;
+                    base[2 * 64 * LD + 64 + threadIdx.x] = dd;
                 }
             }
         }
