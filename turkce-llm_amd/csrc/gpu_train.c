@@ -373,7 +373,7 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
         ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
         {
             void* args[] = { &ap };
-            hip_launch(g->k.attn_fwd, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_fwd, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
         /* x2 = x_in + (att @ Wo + bo) */
         gemm1(g, GEMM_NN, a->att, P_(g, pidx(l, PK_WO)), a->x2, N, D, D, D, D, D, 0.0f, P_(g, pidx(l, PK_BO)),
@@ -443,8 +443,8 @@ static void backward_pass(GpuTrainer* g) {
         ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
         {
             void* args[] = { &ap };
-            hip_launch(g->k.attn_bwd_dq, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
-            hip_launch(g->k.attn_bwd_dkv, cdiv_u64(g->T, 64), g->B * g->H, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
         rope(g, g->dqkv, 1);
         gemm1(g, GEMM_TN, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), D, 3 * D, N, D, 3 * D, 3 * D, 0.0f, NULL,

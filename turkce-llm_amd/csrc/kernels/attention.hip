@@ -55,27 +55,65 @@ template <int HD>
 struct AttTile {
     static constexpr int NQ = 64 * HD / 4 / 256;
     f32x4 v[NQ];
-    // rows >= rlim read as 0 (their address is clamped to row rlim-1, so
-    // every load stays inside the tensor)
+    // Row addresses are clamped to row rlim-1, so every load stays inside the
+    // tensor; rows >= rlim are zeroed by store(), not here, so that a
+    // prefetch does not have to wait for its data.
     __device__ __forceinline__ void load(const float* base, int ld, int r0, int rlim, int col0) {
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             int idx = threadIdx.x + i * 256;
             int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
             int row = r0 + r;
-            bool ok = row < rlim;
-            f32x4 x = *(const f32x4*)(base + (long long)(ok ? row : rlim - 1) * ld + col0 + c);
-            if (!ok) x = f32x4{0.f, 0.f, 0.f, 0.f};
-            v[i] = x;
+            v[i] = *(const f32x4*)(base + (long long)(row < rlim ? row : rlim - 1) * ld + col0 + c);
         }
     }
-    // LDS layout [64][HD + 4]
-    __device__ __forceinline__ void store(float* lds) const {
+    // LDS layout [64][HD + 4]; rows r0 + r >= rlim are written as 0
+    __device__ __forceinline__ void store(float* lds, int r0, int rlim) const {
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             int idx = threadIdx.x + i * 256;
             int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
-            *(f32x4*)(lds + r * (HD + 4) + c) = v[i];
+            f32x4 x = v[i];
+            if (r0 + r >= rlim) x = f32x4{0.f, 0.f, 0.f, 0.f};
+            *(f32x4*)(lds + r * (HD + 4) + c) = x;
+        }
+    }
+};
+
+// A [64 x HD] tile stored transposed in LDS, [HD][ATT_LDT] (row index
+// contiguous), so that 4 consecutive rows of one column are one 128-bit LDS
+// read.  Each load instruction of a wave covers 16 rows x 4 column groups
+// (rows 64 bytes apart in LDS per column), which keeps the transposing
+// 32-bit stores at the minimum two LDS cycles per instruction.
+#define ATT_LDT 68
+template <int HD>
+struct AttTileT {
+    static constexpr int NQ = 64 * HD / 4 / 256;
+    f32x4 v[NQ];
+    __device__ __forceinline__ void coords(int i, int& r, int& c) const {
+        const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+        const int blk = w * NQ + i;
+        r = 16 * (blk & 3) + (l & 15);
+        c = 4 * (4 * (blk >> 2) + (l >> 4));
+    }
+    __device__ __forceinline__ void load(const float* base, int ld, int r0, int rlim, int col0) {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            int r, c;
+            coords(i, r, c);
+            int row = r0 + r;
+            v[i] = *(const f32x4*)(base + (long long)(row < rlim ? row : rlim - 1) * ld + col0 + c);
+        }
+    }
+    __device__ __forceinline__ void store(float* lds, int r0, int rlim) const {
+#pragma unroll
+        for (int i = 0; i < NQ; i++) {
+            int r, c;
+            coords(i, r, c);
+            f32x4 x = v[i];
+            if (r0 + r >= rlim) x = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int e = 0; e < 4; e++) lds[(c + e) * ATT_LDT + r] = x[e];
         }
     }
 };
@@ -99,6 +137,15 @@ __device__ __forceinline__ void att_frag_global(const float* base, int ld, int r
     }
 }
 
+// Make the compiler wait for loaded operand registers here, once: later
+// loads issued inside a loop would otherwise be waited for together with
+// them (the memory counter is in order) at their first use in the loop.
+template <int N>
+__device__ __forceinline__ void att_settle(const f32x4* x) {
+#pragma unroll
+    for (int i = 0; i < N; i++) asm volatile("" ::"v"(x[i]));
+}
+
 // Store a [HD x 32] accumulator set (rows d, one column per lane) to the
 // row of `row` (columns col0 + d): float4 over 4 consecutive d.
 template <int HD>
@@ -118,19 +165,22 @@ __device__ __forceinline__ void att_store_rows(float* rowp, const f32x16* acc, i
 }
 
 // =========================================================== forward
-// grid (ceil(T/64), B*H), 256 threads.  Wave w: query group g = w&1 (32
+// grid (B*H, ceil(T/64)), 256 threads.  Wave w: query group g = w&1 (32
 // queries), key partition part = w>>1 (key blocks part, part+2, ...).
 template <int HD>
 __device__ void flash_fwd(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
     constexpr int LD = HD + 4;
-    __shared__ __attribute__((aligned(16))) float lds[4 * 64 * LD];   // [part][K|V][64][LD]
+    constexpr int KS = 64 * LD, VS = HD * ATT_LDT;                     // K [64][LD], V^T [HD][ATT_LDT]
+    __shared__ __attribute__((aligned(16))) float lds[2 * (KS + VS)];  // [part][K | V^T]
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
     const int grp = wave & 1, part = wave >> 1;
     const int nqb = (p.T + 63) / 64;
-    const int qb = nqb - 1 - (int)blockIdx.x;   // long (late) query blocks first
-    const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
+    // blockIdx.x (dispatched fastest) runs over heads, so every head's
+    // longest (latest) query block is dispatched before any shorter one
+    const int qb = nqb - 1 - (int)blockIdx.y;
+    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
     const float* qkv = p.qkv + rowbase * p.ldq;
     const int qcol = h * HD, kcol = p.D + h * HD, vcol = 2 * p.D + h * HD;
@@ -151,33 +201,34 @@ __device__ void flash_fwd(const AttnParams& p) {
     if (kv_end > p.T) kv_end = p.T;
     const int nkv = (kv_end + 63) / 64;
     const int niter = (nkv + 1) / 2;
-    const float* Ks = lds + part * 2 * 64 * LD;
-    const float* Vs = Ks + 64 * LD;
+    const float* Ks = lds + part * (KS + VS);
+    const float* Vt = Ks + KS;
     // K and V of the stage's two key blocks go through registers, fetched one
     // stage ahead so that their loads overlap the previous stage's MFMAs.
-    AttTile<HD> tk[2], tv[2];
+    // Loads and stores are unconditional (blocks past the end load clamped
+    // rows and store zeros that no wave reads), so the compiler's wait
+    // tracking sees one straight path and never waits for a fetch early.
+    AttTile<HD> tk[2];
+    AttTileT<HD> tv[2];
     auto fetch = [&](int it) {
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const int kb = 2 * it + pp;
-            if (kb < nkv) {
-                tk[pp].load(qkv, p.ldq, kb * 64, p.T, kcol);
-                tv[pp].load(qkv, p.ldq, kb * 64, p.T, vcol);
-            }
+            tk[pp].load(qkv, p.ldq, kb * 64, p.T, kcol);
+            tv[pp].load(qkv, p.ldq, kb * 64, p.T, vcol);
         }
     };
     fetch(0);
+    att_settle<HD / 8>(qf);
     for (int it = 0; it < niter; it++) {
         __syncthreads();
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
-            if (2 * it + pp < nkv) {
-                tk[pp].store(lds + pp * 2 * 64 * LD);
-                tv[pp].store(lds + pp * 2 * 64 * LD + 64 * LD);
-            }
+            tk[pp].store(lds + pp * (KS + VS), (2 * it + pp) * 64, kv_end);
+            tv[pp].store(lds + pp * (KS + VS) + KS, (2 * it + pp) * 64, kv_end);
         }
         __syncthreads();
-        if (it + 1 < niter) fetch(it + 1);
+        fetch(it + 1);
         const int kb = 2 * it + part;
         const int kv0 = kb * 64;
         if (kb >= nkv || kv0 > qw0 + 31) continue;
@@ -223,17 +274,24 @@ __device__ void flash_fwd(const AttnParams& p) {
         for (int d = 0; d < DB; d++)
 #pragma unroll
             for (int r = 0; r < 16; r++) o[d][r] *= alpha;
+        // O^T += V^T P^T: registers 4g..4g+3 of s[c] hold keys
+        // c*32 + 8g + 4*half + (0..3), one 128-bit read of V^T each
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int kr = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+            for (int g = 0; g < 4; g++) {
+                f32x4 vt[DB];
 #pragma unroll
                 for (int d = 0; d < DB; d++) {
                     const int dc = d * 32 + (lane & 31);
-                    float vv = (dc < HD) ? Vs[kr * LD + dc] : 0.f;
-                    o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, s[c][r], o[d], 0, 0, 0);
+                    vt[d] = (dc < HD) ? *(const f32x4*)(Vt + dc * ATT_LDT + c * 32 + 8 * g + 4 * half)
+                                      : f32x4{0.f, 0.f, 0.f, 0.f};
                 }
+#pragma unroll
+                for (int t = 0; t < 4; t++)
+#pragma unroll
+                    for (int d = 0; d < DB; d++)
+                        o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[d][t], s[c][4 * g + t], o[d], 0, 0, 0);
             }
     }
     // merge the two key partitions of each query group: (m, l, O) of part 1
@@ -267,7 +325,7 @@ __device__ void flash_fwd(const AttnParams& p) {
 }
 
 // =========================================================== backward dQ
-// grid (ceil(T/64), B*H).  Same split as the forward: query group x key
+// grid (B*H, ceil(T/64)).  Same split as the forward: query group x key
 // partition; S^T and dP^T put one query per lane; dQ^T += K^T dS^T.  Also
 // writes D_i = <dO_i, O_i> for the dK/dV pass.
 template <int HD>
@@ -279,8 +337,8 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
     const int grp = wave & 1, part = wave >> 1;
     const int nqb = (p.T + 63) / 64;
-    const int qb = nqb - 1 - (int)blockIdx.x;
-    const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
+    const int qb = nqb - 1 - (int)blockIdx.y;     // longest blocks first, as in the forward
+    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
     const float* qkv = p.qkv + rowbase * p.ldq;
     const float* dO = p.dO + rowbase * p.ldo;
@@ -322,20 +380,17 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
     for (int it = 0; it < niter; it++) {
         // K, V of each of the stage's two key blocks: all loads of a block
         // are in flight together, then stored (registers are too scarce
-        // here to fetch a whole stage ahead)
+        // here to fetch a whole stage ahead).  Unconditional, as in the
+        // forward: blocks past the end load clamped rows and store zeros.
 #pragma unroll
         for (int pp = 0; pp < 2; pp++) {
             const int kbp = 2 * it + pp;
             AttTile<HD> tk, tv;
-            if (kbp < nkv) {
-                tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
-                tv.load(qkv, p.ldq, kbp * 64, p.T, vcol);
-            }
+            tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
+            tv.load(qkv, p.ldq, kbp * 64, p.T, vcol);
             if (pp == 0) __syncthreads();
-            if (kbp < nkv) {
-                tk.store(lds + pp * 2 * 64 * LD);
-                tv.store(lds + pp * 2 * 64 * LD + 64 * LD);
-            }
+            tk.store(lds + pp * 2 * 64 * LD, kbp * 64, kv_end);
+            tv.store(lds + pp * 2 * 64 * LD + 64 * LD, kbp * 64, kv_end);
         }
         __syncthreads();
         const int kb = 2 * it + part;
@@ -394,7 +449,7 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
 }
 
 // =========================================================== backward dK, dV
-// grid (ceil(T/64), B*H).  Wave w: key group g = w&1 (32 keys), query
+// grid (B*H, ceil(T/64)).  Wave w: key group g = w&1 (32 keys), query
 // partition part = w>>1 (64-query blocks at or after the keys' block,
 // alternating).  S and dP are formed as [q x kv] (one key per lane), so the
 // P and dS registers feed dV^T += dO^T P and dK^T += Q^T dS directly.
@@ -407,8 +462,8 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
     const int grp = wave & 1, part = wave >> 1;
-    const int kb = blockIdx.x;                               // early keys have the most queries
-    const int bh = blockIdx.y, b = bh / p.H, h = bh - b * p.H;
+    const int kb = blockIdx.y;                               // early keys (most queries) first
+    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
     const float* qkv = p.qkv + rowbase * p.ldq;
     const float* dO = p.dO + rowbase * p.ldo;
@@ -439,31 +494,29 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     for (int it = 0; it < niter; it++) {
         // Q, dO (+ L, D) of the stage's two query blocks, one tile at a time:
         // a tile's loads are in flight together, then stored (the K, V
-        // operands and four accumulators leave room for one tile only)
+        // operands and four accumulators leave room for one tile only).
+        // Unconditional: blocks past the end load clamped rows, store zeros.
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
             const int pp = tt >> 1, jp = 2 * it + pp;
             const bool isq = (tt & 1) == 0;
+            const int q0 = (kb + jp) * 64;
             AttTile<HD> tl;
             float lv = 0.f, dd = 0.f;
-            const int q0 = (kb + jp) * 64;
-            if (jp < nblk) {
-                if (isq) tl.load(qkv, p.ldq, q0, p.T, qcol);
-                else tl.load(dO, p.ldo, q0, p.T, qcol);
-                const int q = q0 + (threadIdx.x & 63);
-                if (isq && threadIdx.x < 64 && q < p.T) {
-                    lv = lse[q];
-                    dd = dv[q];
-                }
+            if (isq) tl.load(qkv, p.ldq, q0, p.T, qcol);
+            else tl.load(dO, p.ldo, q0, p.T, qcol);
+            const int q = q0 + (threadIdx.x & 63);
+            if (isq && threadIdx.x < 64) {
+                const int qc = q < p.T ? q : p.T - 1;
+                lv = lse[qc];
+                dd = dv[qc];
             }
             if (tt == 0) __syncthreads();
-            if (jp < nblk) {
-                float* base = lds + pp * TILE;
-                tl.store(base + (isq ? 0 : 64 * LD));
-                if (isq && threadIdx.x < 64) {
-                    base[2 * 64 * LD + threadIdx.x] = lv;
-                    base[2 * 64 * LD + 64 + threadIdx.x] = dd;
-                }
+            float* base = lds + pp * TILE;
+            tl.store(base + (isq ? 0 : 64 * LD), q0, p.T);
+            if (isq && threadIdx.x < 64) {
+                base[2 * 64 * LD + threadIdx.x] = q < p.T ? lv : 0.f;
+                base[2 * 64 * LD + 64 + threadIdx.x] = q < p.T ? dd : 0.f;
             }
         }
         __syncthreads();
@@ -540,7 +593,9 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dkv_hd##HD(AttnParams p) { \
         flash_bwd_dkv<HD>(p);                                                                             \
     }                                                                                                     \
-    extern "C" __global__ void __launch_bounds__(256) k_attn_bwd_dq_hd##HD(AttnParams p) { flash_bwd_dq<HD>(p); }
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dq_hd##HD(AttnParams p) { \
+        flash_bwd_dq<HD>(p);                                                                              \
+    }
 
 ATT_KERNELS(16)
 ATT_KERNELS(32)
