@@ -61,6 +61,31 @@ const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 ba
  * Returns 0, or -1 for an unknown name (selection is then automatic). */
 i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits);
 
+/* ---- KV-cache decode (generate.c:57-73,186-212 without the per-step
+ * full-window recompute).  The decoder uses the trainer's resident
+ * parameters, kernels, stream and GEMM engine; it owns a K/V cache of
+ * L x batch x H x max_ctx x hd floats each.  All sequences of a batch share
+ * one length.  Errors (tokens outside the vocabulary, a full context, a step
+ * before the prefill) print "[HIP ERROR] gpu_decode: ..." and _exit(1). */
+typedef struct TrlmDecoder TrlmDecoder;
+TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx);
+void gpu_decoder_destroy(TrlmDecoder* d);
+/* ids [batch][len] -> cache positions 0..len-1; logits of position len-1 */
+void gpu_decoder_prefill(TrlmDecoder* d, const u32* ids, u32 len);
+/* ids [batch]: one new token per sequence at position length(); its logits */
+void gpu_decoder_step(TrlmDecoder* d, const u32* ids);
+u32 gpu_decoder_length(const TrlmDecoder* d);
+/* logits of the last prefill/step position, [batch][V] */
+void gpu_decoder_logits(TrlmDecoder* d, f32* host_logits);
+/* first index of each row's maximum */
+void gpu_decoder_greedy(TrlmDecoder* d, u32* out_ids);
+/* sample_next (generate.c:57-73) per row; rngs[batch] each advance by one
+ * pcg_uniform draw, exactly as the reference's loop consumes them */
+void gpu_decoder_sample(TrlmDecoder* d, PCGState* rngs, f32 temperature, u32* out_ids);
+/* prefill + greedy generation of `steps` tokens per sequence; out
+ * [batch][steps] (prompt_len + steps <= max_ctx) */
+void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, u32* out);
+
 /* Stream-event timing on the current context's stream. */
 typedef struct TrlmTimer { hipEvent_t start, stop; } TrlmTimer;
 void trlm_timer_create(TrlmTimer* t);

@@ -71,6 +71,7 @@ def _load():
         "or_adam_step": (None, [f32p, f32p, f32p, f32p, C.c_uint64, C.c_uint64, C.c_float,
                                 C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]),
         "or_argmax": (C.c_uint32, [f32p, C.c_uint32]),
+        "or_sample_next": (C.c_uint32, [f32p, C.c_uint32, C.c_float, C.POINTER(Pcg), f32p]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -169,6 +170,13 @@ def pcg_stream(seed_a, seed_b):
     r = Pcg()
     lib().or_pcg_seed(C.byref(r), seed_a, seed_b)
     return r
+
+
+def sample_next(row, temperature, pcg):
+    """sample_next on one row of logits; pcg (a Pcg) advances by one draw."""
+    row = np.ascontiguousarray(row, np.float32)
+    scratch = np.zeros(row.size, np.float32)
+    return int(lib().or_sample_next(row, row.size, temperature, C.byref(pcg), scratch))
 
 
 def random_tokens(n, V, seed_a=4242, seed_b=7, hi_exclusive=None):

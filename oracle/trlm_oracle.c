@@ -319,6 +319,28 @@ uint32_t or_argmax(const float* row, uint32_t n) {
     return best;
 }
 
+/* sample_next (training/generate.c:57-73): max of the row; e_j =
+ * m_expf((z_j - max) / temperature) summed in f64 in index order;
+ * r = pcg_uniform * sum (prng.c:33-36); the first j whose running f64 sum
+ * reaches r, else n - 1. */
+uint32_t or_sample_next(const float* logits, uint32_t n, float temperature, OrPcg* rng, float* scratch) {
+    float mx = logits[0];
+    for (uint32_t j = 1; j < n; j++) if (logits[j] > mx) mx = logits[j];
+    double sum = 0.0;
+    for (uint32_t j = 0; j < n; j++) {
+        float e = or_m_expf((logits[j] - mx) / temperature);
+        scratch[j] = e;
+        sum += (double)e;
+    }
+    double r = (double)or_pcg_next_u32(rng) * (1.0 / 4294967296.0) * sum;
+    double c = 0.0;
+    for (uint32_t j = 0; j < n; j++) {
+        c += (double)scratch[j];
+        if (c >= r) return j;
+    }
+    return n - 1;
+}
+
 /* ======================= dense kernels ======================= */
 
 /* C[M,N] (+)= A @ B where B rows are contiguous (row stride ldb).  Each

@@ -88,5 +88,7 @@ void or_adam_step(float* p, const float* g, float* m, float* v, uint64_t n, uint
                   float lr, float b1, float b2, float eps, float wd, float grad_scale);
 
 uint32_t or_argmax(const float* row, uint32_t n);
+/* sample_next (training/generate.c:57-73) on one row of logits; scratch [n]. */
+uint32_t or_sample_next(const float* logits, uint32_t n, float temperature, OrPcg* rng, float* scratch);
 
 #endif

@@ -91,8 +91,8 @@ def test_undefined_symbols_are_runtime_only(trlm):
                          check=True).stdout
     names = {ln.split()[-1].split("@")[0] for ln in out.splitlines() if ln.strip()}
     runtime = {"allocator_alloc", "tensor_create", "tensor_transpose", "tensor_contiguous", "tensor_add_inplace",
-               "node_make_custom", "rope_build_tables", "pcg_seed", "pcg_range_i64", "m_powf", "m_sqrt",
-               "m_sqrtf"}
+               "node_make_custom", "rope_build_tables", "pcg_seed", "pcg_range_i64", "pcg_next_u32", "m_powf",
+               "m_sqrt", "m_sqrtf"}
     other = {n for n in names if not (n.startswith("hip") or n.startswith("_") or n in runtime)}
     libc = {"fprintf", "fflush", "_exit", "fopen", "fseek", "ftell", "fread", "fclose", "malloc", "calloc",
             "realloc", "free", "memset", "memcpy", "strcmp", "snprintf", "stderr", "stdout", "clock_gettime",
@@ -105,11 +105,12 @@ def test_code_object_has_every_kernel(trlm):
     with open(trlm.KERNELS, "rb") as fh:
         blob = fh.read()
     src = ""
-    for f in ("gpu_train.c", "trlm_gemm.c"):
+    for f in ("gpu_train.c", "gpu_decode.c", "trlm_gemm.c"):
         src += open(os.path.join(ROOT, "turkce-llm_amd", "csrc", f)).read()
     names = set(re.findall(r'"(k_[a-z0-9_]+)"', src))
     names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_decode_attn_hd%d" % d for d in (16, 32, 64)} | {"k_decode_merge_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in (
         "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32")}
     names |= {"k_gemm_%s_64x64_u" % l for l in ("nn", "nt", "tn", "tt")}

@@ -1,0 +1,156 @@
+"""KV-cache decode (additive API) through the C ABI.
+
+The reference generates by recomputing the full window each step and reading
+the last row (training/generate.c:186-212).  Within the context (no window
+slide) that last row is what the decoder must produce, so:
+  - after the prefill and after every step, the decoder's logits equal the
+    oracle's full forward over the whole context at its last position, within
+    1e-4 of max|logits| (head_dim 16, 32, 64; contexts crossing the
+    256-key chunks of the decode attention);
+  - greedy picks are the first maximum of those logits; generate_greedy
+    equals prefill + greedy + step by hand, bit for bit;
+  - sampling follows sample_next (generate.c:57-73) bit for bit: the oracle's
+    restatement, run on the decoder's own logits with the same PCG streams,
+    picks the same tokens and leaves the streams in the same state;
+  - at the real architecture (V 31769, D 384, L 12) the decoder equals the
+    GPU trainer's full forward (itself pinned to the oracle) at the last
+    position, within 1e-4.
+"""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def rel_err(got, want):
+    return float(np.abs(got.astype(np.float64) - want).max() / np.abs(want).max())
+
+
+def last_rows(orc, model, params, ctx, B):
+    """Oracle logits of the last position of each sequence, ctx [B, T]."""
+    T = ctx.shape[1]
+    full = model.forward_logits(params, np.ascontiguousarray(ctx, np.uint32).ravel(), B, T)
+    return full.reshape(B, T, -1)[:, -1, :]
+
+
+@pytest.mark.parametrize("V,D,H,L,F,B,P,S", [
+    (61, 32, 2, 2, 48, 3, 5, 6),       # head_dim 16
+    (97, 64, 2, 2, 96, 2, 9, 5),       # head_dim 32
+    (83, 128, 2, 2, 160, 2, 7, 4),     # head_dim 64
+    (71, 128, 2, 1, 64, 2, 250, 12),   # keys cross the 256-key chunk boundary
+])
+def test_decode_equals_full_recompute(trlm, orc, V, D, H, L, F, B, P, S):
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, B, P + S + 1)
+    try:
+        dec.prefill(prompt)
+        ctx = prompt.copy()
+        worst = 0.0
+        for s in range(S + 1):
+            got = dec.logits()
+            want = last_rows(orc, model, params, ctx, B)
+            err = rel_err(got, want)
+            worst = max(worst, err)
+            assert err <= 1e-4, (s, err)
+            nxt = dec.greedy()
+            assert np.array_equal(nxt, np.argmax(got, axis=1).astype(np.uint32))
+            assert dec.length() == ctx.shape[1]
+            if s < S:
+                dec.step(nxt)
+                ctx = np.concatenate([ctx, nxt[:, None]], axis=1)
+        print("decode V%d D%d P%d S%d: worst rel err %.2e" % (V, D, P, S, worst))
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+
+
+def test_generate_greedy_matches_manual_loop(trlm, orc):
+    V, D, H, L, F, B, P, S = 67, 64, 2, 2, 96, 3, 6, 7
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    d1 = trlm.Decoder(tr, B, P + S)
+    d2 = trlm.Decoder(tr, B, P + S)
+    try:
+        gen = d1.generate_greedy(prompt, S)
+        d2.prefill(prompt)
+        manual = []
+        for s in range(S):
+            nxt = d2.greedy()
+            manual.append(nxt)
+            if s + 1 < S:
+                d2.step(nxt)
+        assert np.array_equal(gen, np.stack(manual, axis=1))
+    finally:
+        d1.destroy()
+        d2.destroy()
+        tr.destroy()
+        hm.close()
+
+
+def test_sampling_follows_sample_next(trlm, orc):
+    V, D, H, L, F, B, P = 113, 64, 2, 2, 96, 4, 5
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, B, P + 10)
+    rngs = (trlm.PCGState * B)(*[trlm.libs()[0].pcg_seed(4242, 7 + b) for b in range(B)])
+    mirror = [orc.pcg_stream(4242, 7 + b) for b in range(B)]
+    try:
+        dec.prefill(prompt)
+        for step in range(8):
+            logits = dec.logits()
+            for temp in (0.85,):
+                got = dec.sample(rngs, temp)
+                want = [orc.sample_next(logits[b], temp, mirror[b]) for b in range(B)]
+                assert list(got) == want, (step, list(got), want)
+                for b in range(B):
+                    assert rngs[b].state == mirror[b].state and rngs[b].inc == mirror[b].inc
+            dec.step(got)
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+
+
+def test_real_architecture_against_gpu_full_forward(trlm, orc):
+    """V 31769, D 384, H 6, L 12, F 1024: batch 4, prompt 100, 3 steps; the
+    decoder's logits at the last position equal the trainer's full forward
+    (B=4, T=len) within 1e-4 of max|logits|."""
+    V, D, H, L, F, B, P, S = 31769, 384, 6, 12, 1024, 4, 100, 3
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, B, P + S + 1)
+    try:
+        dec.prefill(prompt)
+        ctx = prompt.copy()
+        for s in range(S + 1):
+            got = dec.logits()
+            full = trlm.Trainer(hm, B, ctx.shape[1])
+            try:
+                want = full.forward_logits(ctx.ravel()).reshape(B, ctx.shape[1], V)[:, -1, :]
+            finally:
+                full.destroy()
+            err = rel_err(got, want)
+            assert err <= 1e-4, (s, err)
+            nxt = dec.greedy()
+            if s < S:
+                dec.step(nxt)
+                ctx = np.concatenate([ctx, nxt[:, None]], axis=1)
+        print("real-scale decode: last rel err %.2e" % err)
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()

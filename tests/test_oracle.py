@@ -238,3 +238,40 @@ def test_sample_batch_windows(orc):
         r = orc.pcg_stream(9 * 1000003 + w, 99 + w)
         start = orc.lib().or_pcg_range_i64(C.byref(r), 0, 5000 - 50 - 1)
         assert np.array_equal(ids[w], toks[start:start + 50])
+
+
+def test_sample_next_closed_forms(orc):
+    """or_sample_next (generate.c:57-73) against cases whose answer does not
+    need the formula: equal logits give weights exactly 1, so the pick is
+    ceil(u*V) - 1 for the stream's uniform u; a single finite logit among
+    -1e30 ones is always picked; with two logits the pick is 0 exactly when
+    e0 >= u*(e0 + e1), e_j = m_expf((z_j - max)/T)."""
+    import ctypes as C
+    import math
+    L = orc.lib()
+    V = 1000
+    for seed in range(40):
+        p = orc.pcg_stream(seed, 3)
+        q = orc.pcg_stream(seed, 3)
+        got = orc.sample_next(np.zeros(V, np.float32), 0.85, p)
+        u = L.or_pcg_next_u32(C.byref(q)) / 4294967296.0
+        assert got == max(0, math.ceil(u * V) - 1)
+        assert p.state == q.state            # exactly one draw consumed
+    for k in (0, 17, 999):
+        z = np.full(V, -1e30, np.float32)
+        z[k] = 3.0
+        for seed in range(10):
+            assert orc.sample_next(z, 0.7, orc.pcg_stream(seed, 5)) == k
+    z = np.array([1.25, 0.5], np.float32)
+    T = 0.85
+    e0 = float(L.or_m_expf(np.float32((z[0] - z[0]) / np.float32(T))))
+    e1 = float(L.or_m_expf(np.float32((z[1] - z[0]) / np.float32(T))))
+    picks = []
+    for seed in range(200):
+        p = orc.pcg_stream(seed, 9)
+        q = orc.pcg_stream(seed, 9)
+        got = orc.sample_next(z, T, p)
+        u = L.or_pcg_next_u32(C.byref(q)) / 4294967296.0
+        assert got == (0 if e0 >= u * (e0 + e1) else 1)
+        picks.append(got)
+    assert 0 < sum(picks) < 200

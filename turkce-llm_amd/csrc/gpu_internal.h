@@ -1,0 +1,37 @@
+/* gpu_internal.h -- pieces of the GPU trainer (gpu_train.c) that the KV-cache
+ * decoder (gpu_decode.c) reuses.  Not part of the C ABI: every symbol here has
+ * hidden visibility in libtrlm_hip.so. */
+#ifndef TRLM_GPU_INTERNAL_H
+#define TRLM_GPU_INTERNAL_H
+
+#include "trlm_ext.h"
+
+#pragma GCC visibility push(hidden)
+
+/* lm_collect_params order (model/gpu_train.c:8-13): [0] embedding; layer l
+ * at 1 + 10*l + k; last = final norm weight. */
+enum { PK_ATTN_NORM = 0, PK_WQKV, PK_BQKV, PK_WO, PK_BO, PK_FFN_NORM, PK_WGU, PK_BGU, PK_WDOWN, PK_BDOWN };
+static inline u32 trlm_pidx(u32 layer, u32 k) { return 1u + 10u * layer + k; }
+
+typedef enum { GEMM_NN, GEMM_NT, GEMM_TN } GemmKind;
+
+/* Called after a layer's QKV projection and RoPE, with that layer's qkv
+ * ([g->N, 3D]: rotated Q, rotated K, V). */
+typedef void (*TrlmLayerHook)(void* ctx, GpuTrainer* g, u32 layer, hipDeviceptr_t qkv);
+
+void trlm_bind(GpuTrainer* g);
+hipDeviceptr_t trlm_param_ptr(const GpuTrainer* g, u32 i);
+/* Embedding, L blocks and final norm over g->N = g->B * g->T rows; the
+ * result is left in g->nf. */
+void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void* hook_ctx);
+void trlm_rmsnorm_rows(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv,
+                       u32 rows);
+void trlm_gemm_rows(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C, i32 M, i32 N,
+                    i32 K, i32 lda, i32 ldb, i32 ldc, hipDeviceptr_t bias, hipDeviceptr_t resid);
+void trlm_swiglu_rows(GpuTrainer* g, hipDeviceptr_t gu, hipDeviceptr_t h, u32 rows);
+void trlm_embed_rows(GpuTrainer* g, hipDeviceptr_t ids, hipDeviceptr_t x, u32 rows);
+void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hipDeviceptr_t out);
+
+#pragma GCC visibility pop
+
+#endif

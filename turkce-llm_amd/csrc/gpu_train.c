@@ -19,12 +19,9 @@
 #include <unistd.h>
 
 #include "trlm_ext.h"
+#include "gpu_internal.h"
 
-/* lm_collect_params order (model/gpu_train.c:8-13): [0] embedding; layer l
- * at 1 + 10*l + k; last = final norm weight. */
-enum { PK_ATTN_NORM = 0, PK_WQKV, PK_BQKV, PK_WO, PK_BO, PK_FFN_NORM, PK_WGU, PK_BGU, PK_WDOWN, PK_BDOWN };
-
-static u32 pidx(u32 layer, u32 k) { return 1u + 10u * layer + k; }
+static u32 pidx(u32 layer, u32 k) { return trlm_pidx(layer, k); }
 
 #define F4 ((u64)sizeof(f32))
 
@@ -54,7 +51,6 @@ static void fill_zero(GpuTrainer* g, hipDeviceptr_t p, u64 n) {
 
 /* C[M,N] = op(A) op(B) (+ beta C) (+ bias) (+ resid), single matrices with
  * the reference's leading-dimension conventions (gpu_train.c:53-63). */
-typedef enum { GEMM_NN, GEMM_NT, GEMM_TN } GemmKind;
 
 static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C, i32 M, i32 N,
                   i32 K, i32 lda, i32 ldb, i32 ldc, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid) {
@@ -62,11 +58,16 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
               bias, resid, ldc);
 }
 
-static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv) {
-    i32 rows = (i32)g->N, cols = (i32)g->D;
+static void rmsnorm_rows(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv,
+                         u32 nrows) {
+    i32 rows = (i32)nrows, cols = (i32)g->D;
     f32 eps = g->eps;
     void* args[] = { &x, &w, &out, &rinv, &rows, &cols, &eps };
-    hip_launch(g->k.rmsnorm_fwd, cdiv_u64(g->N, 4), 1, 1, 256, 1, 1, 0, args);
+    hip_launch(g->k.rmsnorm_fwd, cdiv_u64(nrows, 4), 1, 1, 256, 1, 1, 0, args);
+}
+
+static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv) {
+    rmsnorm_rows(g, x, w, out, rinv, g->N);
 }
 
 #define RMS_ROWS 16u
@@ -352,8 +353,10 @@ static void check_ids(const GpuTrainer* g, const u32* ids, const char* what) {
         }
 }
 
-static void forward_to_logits(GpuTrainer* g, const u32* ids) {
-    i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F, V = (i32)g->V, ldv = (i32)g->ldv;
+/* Embedding, the L blocks and the final norm (-> g->nf).  hook (if any) runs
+ * after each layer's QKV projection and RoPE, with that layer's qkv. */
+void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void* hook_ctx) {
+    i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F;
     check_ids(g, ids, "ids");
     hip_h2d(g->ids, ids, (u64)N * sizeof(u32));
     {
@@ -370,6 +373,7 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
         gemm1(g, GEMM_NN, a->n1, P_(g, pidx(l, PK_WQKV)), a->qkv, N, 3 * D, D, D, 3 * D, 3 * D, 0.0f,
               P_(g, pidx(l, PK_BQKV)), NULL);
         rope(g, a->qkv, 0);
+        if (hook) hook(hook_ctx, g, l, a->qkv);
         ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
         {
             void* args[] = { &ap };
@@ -391,6 +395,11 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
               a->x2);
     }
     rmsnorm_fwd(g, g->x_final, P_(g, pidx(g->L, 0)), g->nf, g->rf);
+}
+
+static void forward_to_logits(GpuTrainer* g, const u32* ids) {
+    i32 N = (i32)g->N, D = (i32)g->D, V = (i32)g->V, ldv = (i32)g->ldv;
+    trlm_forward_hidden(g, ids, NULL, NULL);
     /* logits = nf @ E^T  (tied head, NT with B = E [V, D]) */
     gemm1(g, GEMM_NT, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 0.0f, NULL, NULL);
 }
@@ -564,4 +573,40 @@ void gpu_trainer_greedy_argmax(GpuTrainer* g, u32* host_ids_out) {
 
 void gpu_trainer_adamw_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay, f32 grad_scale) {
     adam_launch(g, opt, grad_scale, weight_decay);
+}
+
+/* ---------------- helpers shared with the decoder (gpu_decode.c) ---------------- */
+
+void trlm_bind(GpuTrainer* g) { bind(g); }
+
+hipDeviceptr_t trlm_param_ptr(const GpuTrainer* g, u32 i) { return P_(g, i); }
+
+void trlm_rmsnorm_rows(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv,
+                       u32 rows) {
+    rmsnorm_rows(g, x, w, out, rinv, rows);
+}
+
+void trlm_gemm_rows(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C, i32 M, i32 N,
+                    i32 K, i32 lda, i32 ldb, i32 ldc, hipDeviceptr_t bias, hipDeviceptr_t resid) {
+    gemm1(g, kind, A, B, C, M, N, K, lda, ldb, ldc, 0.0f, bias, resid);
+}
+
+void trlm_swiglu_rows(GpuTrainer* g, hipDeviceptr_t gu, hipDeviceptr_t h, u32 rows) {
+    i32 n = (i32)rows, F = (i32)g->F;
+    void* args[] = { &gu, &h, &n, &F };
+    hip_launch(g->k.swiglu_fwd, cdiv_u64((u64)rows * g->F, 256), 1, 1, 256, 1, 1, 0, args);
+}
+
+void trlm_embed_rows(GpuTrainer* g, hipDeviceptr_t ids, hipDeviceptr_t x, u32 rows) {
+    hipDeviceptr_t E = P_(g, 0);
+    i32 n = (i32)rows, D = (i32)g->D;
+    void* args[] = { &E, &ids, &x, &n, &D };
+    u64 work = (g->D % 4 == 0) ? (u64)rows * g->D / 4 : (u64)rows * g->D;
+    hip_launch(g->k.embed_fwd, cdiv_u64(work, 256), 1, 1, 256, 1, 1, 0, args);
+}
+
+void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hipDeviceptr_t out) {
+    i32 V = (i32)g->V;
+    void* args[] = { &logits, &ld, &V, &out };
+    hip_launch(g->k.argmax_rows, rows, 1, 1, 256, 1, 1, 0, args);
 }

@@ -4,3 +4,4 @@
 #include "gemm.hip"
 #include "rowops.hip"
 #include "attention.hip"
+#include "decode.hip"

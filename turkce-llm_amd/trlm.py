@@ -163,6 +163,17 @@ def _bind(host, hip):
     _sig(hip, "gpu_trainer_forward_logits", None, [GP, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_forward_loss_logits", C.c_float, [GP, u32p, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_greedy_argmax", None, [GP, u32p])
+    DP = C.c_void_p
+    f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
+    _sig(hip, "gpu_decoder_create", DP, [GP, C.c_uint32, C.c_uint32])
+    _sig(hip, "gpu_decoder_destroy", None, [DP])
+    _sig(hip, "gpu_decoder_prefill", None, [DP, u32p, C.c_uint32])
+    _sig(hip, "gpu_decoder_step", None, [DP, u32p])
+    _sig(hip, "gpu_decoder_length", C.c_uint32, [DP])
+    _sig(hip, "gpu_decoder_logits", None, [DP, f32p])
+    _sig(hip, "gpu_decoder_greedy", None, [DP, u32p])
+    _sig(hip, "gpu_decoder_sample", None, [DP, C.POINTER(PCGState), C.c_float, u32p])
+    _sig(hip, "gpu_decoder_generate_greedy", None, [DP, u32p, C.c_uint32, C.c_uint32, u32p])
 
     HP = C.POINTER(HipCtx)
     _sig(hip, "hip_init", HipCtx, [AP, C.c_char_p])
@@ -383,6 +394,53 @@ class Trainer:
         if self.g is not None:
             self.hip.gpu_trainer_destroy(C.byref(self.g))
             self.g = None
+
+
+class Decoder:
+    """gpu_decoder_* (KV-cache decode) over a Trainer's resident parameters."""
+
+    def __init__(self, trainer, batch, max_ctx):
+        self.hip = trainer.hip
+        self.tr = trainer
+        self.B, self.V = batch, trainer.hm.V
+        self.d = self.hip.gpu_decoder_create(C.byref(trainer.g), batch, max_ctx)
+
+    def prefill(self, ids):
+        ids = _u32(ids)
+        self.hip.gpu_decoder_prefill(self.d, ids.ravel(), ids.shape[-1] if ids.ndim > 1 else ids.size // self.B)
+
+    def step(self, ids):
+        self.hip.gpu_decoder_step(self.d, _u32(ids).ravel())
+
+    def length(self):
+        return self.hip.gpu_decoder_length(self.d)
+
+    def logits(self):
+        out = np.zeros((self.B, self.V), np.float32)
+        self.hip.gpu_decoder_logits(self.d, out)
+        return out
+
+    def greedy(self):
+        out = np.zeros(self.B, np.uint32)
+        self.hip.gpu_decoder_greedy(self.d, out)
+        return out
+
+    def sample(self, rngs, temperature):
+        """rngs: ctypes array of PCGState (one per sequence), advanced in place."""
+        out = np.zeros(self.B, np.uint32)
+        self.hip.gpu_decoder_sample(self.d, rngs, temperature, out)
+        return out
+
+    def generate_greedy(self, prompt, steps):
+        prompt = _u32(prompt)
+        out = np.zeros((self.B, steps), np.uint32)
+        self.hip.gpu_decoder_generate_greedy(self.d, prompt.ravel(), prompt.shape[-1], steps, out)
+        return out
+
+    def destroy(self):
+        if self.d is not None:
+            self.hip.gpu_decoder_destroy(self.d)
+            self.d = None
 
 
 def _u32(a):
