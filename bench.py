@@ -163,6 +163,45 @@ def model_benchmarks(trlm, steps, warmup):
     return out
 
 
+DEC_B, DEC_PROMPT, DEC_CTX = 64, 128, 1024
+
+
+def decode_benchmark(trlm):
+    """Config 5: 64 sequences, 128-token prompts (ids pcg_range_i64(0, V) from
+    pcg_seed(4242, 9)), greedy KV-cache decode to context 1024: 896 new tokens
+    per sequence (prefill + 895 steps), random-init weights of the real
+    architecture.  Bytes per step = all weights (133.96 MB) + the K and V
+    cache read by the step (64*12*2*ctx*384*4 B)."""
+    host, _ = trlm.libs()
+    import ctypes as C
+    rng = np.random.default_rng(11)
+    params = model_params(rng)
+    pcg = host.pcg_seed(4242, 9)
+    prompt = np.array([host.pcg_range_i64(C.byref(pcg), 0, V) for _ in range(DEC_B * DEC_PROMPT)],
+                      np.uint32).reshape(DEC_B, DEC_PROMPT)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, DEC_B, DEC_CTX)
+    try:
+        dec.generate_greedy(prompt, 16)       # warm-up (kernels, workspaces, prefill buffers)
+        steps = DEC_CTX - DEC_PROMPT
+        t0 = time.perf_counter()
+        dec.generate_greedy(prompt, steps)
+        dt = time.perf_counter() - t0
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+    weights = 4.0 * (V * D + L * (2 * D + 3 * D * D + 3 * D + D * D + D + 2 * D * F + 2 * F + F * D + D) + D)
+    kv = sum(DEC_B * L * 2 * n * D * 4.0 for n in range(DEC_PROMPT + 1, DEC_CTX + 1))
+    total = weights * (steps - 1) + kv - DEC_B * L * 2 * DEC_CTX * D * 4.0
+    tokens = DEC_B * steps
+    return {"decode_tokens_per_s": tokens / dt, "decode_ms_per_token": dt * 1e3 / steps,
+            "decode_gbps": total / dt / 1e9, "decode_total_s": dt,
+            "decode_config": "batch %d, prompt %d, greedy to context %d (%d steps)" % (
+                DEC_B, DEC_PROMPT, DEC_CTX, steps - 1)}
+
+
 def cpu_baseline(seconds_target=10.0):
     """Reference tensor_matmul2d (or the oracle) on QKV-shaped rows."""
     import oracle
@@ -278,6 +317,7 @@ def main():
     ap.add_argument("--tune", action="store_true",
                     help="time every GEMM tile variant / split-K factor on the sweep shapes and exit")
     ap.add_argument("--tune-out", default=None, help="with --tune: write every timing as JSON lines here")
+    ap.add_argument("--decode-only", action="store_true", help="only the config-5 decode measurement (JSON line)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
@@ -288,6 +328,9 @@ def main():
     _, hip = trlm.libs()
     if args.tune:
         tune(trlm, hip, max(3, args.steps // 2), args.tune_out)
+        return
+    if args.decode_only:
+        print(json.dumps(decode_benchmark(trlm)), flush=True)
         return
     if args.model_only:
         print(json.dumps(model_benchmarks(trlm, args.steps, args.warmup)), flush=True)
@@ -333,6 +376,9 @@ def main():
         log("model: forward / train at B=%d T=%d" % (B, T))
         line.update({k: (round(v, 3) if isinstance(v, float) else v)
                      for k, v in model_benchmarks(trlm, max(3, args.steps // 2), args.warmup).items()})
+    if not args.no_model:
+        log("decode: config 5")
+        line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode_benchmark(trlm).items()})
     if not args.no_cpu:
         log("cpu baseline leg")
         cb = cpu_baseline()

@@ -6,7 +6,7 @@ slide) that last row is what the decoder must produce, so:
   - after the prefill and after every step, the decoder's logits equal the
     oracle's full forward over the whole context at its last position, within
     1e-4 of max|logits| (head_dim 16, 32, 64; contexts crossing the
-    256-key chunks of the decode attention);
+    256-key chunks of the decode attention; batches 2 to 65);
   - greedy picks are the first maximum of those logits; generate_greedy
     equals prefill + greedy + step by hand, bit for bit;
   - sampling follows sample_next (generate.c:57-73) bit for bit: the oracle's
@@ -38,6 +38,7 @@ def last_rows(orc, model, params, ctx, B):
     (97, 64, 2, 2, 96, 2, 9, 5),       # head_dim 32
     (83, 128, 2, 2, 160, 2, 7, 4),     # head_dim 64
     (71, 128, 2, 1, 64, 2, 250, 12),   # keys cross the 256-key chunk boundary
+    (53, 32, 2, 1, 32, 65, 3, 2),      # batch 65
 ])
 def test_decode_equals_full_recompute(trlm, orc, V, D, H, L, F, B, P, S):
     model = orc.Model(V, D, H, L, F)
@@ -150,6 +151,40 @@ def test_real_architecture_against_gpu_full_forward(trlm, orc):
                 dec.step(nxt)
                 ctx = np.concatenate([ctx, nxt[:, None]], axis=1)
         print("real-scale decode: last rel err %.2e" % err)
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+
+
+def test_replayed_steps_survive_training_and_new_prompts(trlm, orc):
+    """Steps after the first replay a captured step.  Interleaving a training
+    step of the same trainer (its GEMM workspace grows), and a second prefill
+    with a new prompt, must leave later steps exact: every step is checked
+    against the oracle's full recompute."""
+    V, D, H, L, F, B, P = 89, 64, 2, 2, 96, 3, 6
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 4, 64)
+    dec = trlm.Decoder(tr, B, 32)
+    toks = orc.random_tokens(4000, V)
+    ids_t, tgt_t = orc.sample_batch(toks, 64, 4, 5)
+    try:
+        for trial in range(2):
+            prompt = orc.random_tokens(B * P, V, 4242, 20 + trial).reshape(B, P)
+            dec.prefill(prompt)
+            ctx = prompt.copy()
+            for s in range(5):
+                want = last_rows(orc, model, params, ctx, B)
+                assert rel_err(dec.logits(), want) <= 1e-4, (trial, s)
+                nxt = dec.greedy()
+                dec.step(nxt)
+                ctx = np.concatenate([ctx, nxt[:, None]], axis=1)
+                if s == 2:
+                    tr.forward_backward(ids_t, tgt_t)   # no optimizer step: weights unchanged
+            want = last_rows(orc, model, params, ctx, B)
+            assert rel_err(dec.logits(), want) <= 1e-4, (trial, "last")
     finally:
         dec.destroy()
         tr.destroy()

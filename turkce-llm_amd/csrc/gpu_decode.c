@@ -47,7 +47,17 @@ struct TrlmDecoder {
     /* prefill buffers, grown to batch x len rows on demand */
     u64 pre_rows;
     hipDeviceptr_t p_x, p_x2, p_n, p_r1, p_r2, p_qkv, p_att, p_lse, p_gu, p_h, p_nf, p_rf, p_ids;
-    hipFunction_t k_fill, k_append, k_attn, k_merge, k_gather, k_sample;
+    hipFunction_t k_fill, k_append, k_attn, k_merge, k_gather, k_sample, k_advance, k_argmax_hist;
+    /* step replay: the position lives on the device (pos_dev), the attention
+     * grid is fixed at nsplit_max, and the step's GEMMs use the decoder's own
+     * engine, so every step is the same launch sequence -- captured once as
+     * a HIP graph after one eager step has sized the GEMM workspace */
+    hipDeviceptr_t pos_dev, hist;
+    u32 hist_cap;
+    TrlmGemm* gemm;
+    u32 eager_steps;
+    hipGraph_t graph;
+    hipGraphExec_t exec;
 };
 
 static void dec_fatal(const char* msg) {
@@ -125,6 +135,10 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->k_merge = hip_get_kernel(c, name);
     d->k_gather = hip_get_kernel(c, "k_gather_rows");
     d->k_sample = hip_get_kernel(c, "k_sample_rows");
+    d->k_advance = hip_get_kernel(c, "k_decode_advance");
+    d->k_argmax_hist = hip_get_kernel(c, "k_argmax_hist");
+    d->pos_dev = hip_alloc(sizeof(i32));
+    d->gemm = trlm_gemm_create(c);
     return d;
 }
 
@@ -136,10 +150,20 @@ static void free_prefill(TrlmDecoder* d) {
     d->pre_rows = 0;
 }
 
+static void drop_graph(TrlmDecoder* d) {
+    if (d->exec) { hipGraphExecDestroy(d->exec); d->exec = NULL; }
+    if (d->graph) { hipGraphDestroy(d->graph); d->graph = NULL; }
+}
+
 void gpu_decoder_destroy(TrlmDecoder* d) {
     if (!d) return;
     trlm_bind(d->g);
+    hip_sync();
+    drop_graph(d);
     free_prefill(d);
+    if (d->hist) hip_free(d->hist);
+    hip_free(d->pos_dev);
+    trlm_gemm_destroy(d->gemm);
     hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->n, d->r, d->qkv, d->att, d->gu, d->h, d->nf,
                               d->logits, d->part, d->out_ids, d->e, d->prefix, d->u, d->cos_t, d->sin_t };
     for (u32 i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) hip_free(bufs[i]);
@@ -224,58 +248,92 @@ void gpu_decoder_prefill(TrlmDecoder* d, const u32* ids, u32 len) {
     }
     head(d);
     d->len = len;
+    i32 lenv = (i32)len;
+    hip_h2d(d->pos_dev, &lenv, sizeof(i32));
 }
 
-void gpu_decoder_step(TrlmDecoder* d, const u32* ids) {
-    GpuTrainer* g = d->g;
-    if (d->len == 0) dec_fatal("step before prefill");
-    if (d->len >= d->ctx) dec_fatal("context is full (max_ctx reached)");
-    check_tokens(d, ids, d->B);
-    trlm_bind(g);
-    const u32 B = d->B, pos = d->len;
+/* One decode step on the device: embed d->ids at position *pos_dev, the L
+ * blocks with the cache append and decode attention, final norm, head into
+ * d->logits, *pos_dev += 1.  Every argument is the same from step to step. */
+static void step_body(TrlmDecoder* d) {
+    GpuTrainer ps = *d->g;   /* the trainer's kernels and parameters, the decoder's GEMM engine */
+    ps.gemm = d->gemm;
+    GpuTrainer* g = &ps;
+    const u32 B = d->B;
     const i32 Bi = (i32)B, D = (i32)d->D, F = (i32)d->F, H = (i32)d->H, hd = (i32)d->hd, ldq = 3 * D;
-    const i32 ctxn = (i32)d->ctx, posi = (i32)pos;
-    hip_h2d(d->ids, ids, (u64)B * sizeof(u32));
+    const i32 ctxn = (i32)d->ctx, chunk = (i32)DEC_CHUNK, nsg = (i32)d->nsplit_max;
+    hipDeviceptr_t posd = d->pos_dev;
     trlm_embed_rows(g, d->ids, d->x, B);
-    const u32 nkeys = pos + 1;
-    const u32 nsplit = cdiv32(nkeys, DEC_CHUNK);
     u64 per_layer = (u64)B * d->H * d->ctx * d->hd;
     for (u32 l = 0; l < d->L; l++) {
         hipDeviceptr_t kc = at(d->kc, l * per_layer), vc = at(d->vc, l * per_layer);
-        trlm_rmsnorm_rows(g, d->x, trlm_param_ptr(g, trlm_pidx(l, PK_ATTN_NORM)), d->n, d->r, B);
-        trlm_gemm_rows(g, GEMM_NN, d->n, trlm_param_ptr(g, trlm_pidx(l, PK_WQKV)), d->qkv, Bi, 3 * D, D, D, 3 * D,
-                       3 * D, trlm_param_ptr(g, trlm_pidx(l, PK_BQKV)), NULL);
+#define PP(k) trlm_param_ptr(g, trlm_pidx(l, k))
+        trlm_rmsnorm_rows(g, d->x, PP(PK_ATTN_NORM), d->n, d->r, B);
+        trlm_gemm_rows(g, GEMM_NN, d->n, PP(PK_WQKV), d->qkv, Bi, 3 * D, D, D, 3 * D, 3 * D, PP(PK_BQKV), NULL);
         {
             hipDeviceptr_t qkv = d->qkv, ct = d->cos_t, st = d->sin_t;
-            void* args[] = { &qkv, (void*)&ldq, &ct, &st, (void*)&posi, (void*)&Bi, (void*)&H, (void*)&hd,
-                             (void*)&D, &kc, &vc, (void*)&ctxn };
+            void* args[] = { &qkv, (void*)&ldq, &ct, &st, &posd, (void*)&Bi, (void*)&H, (void*)&hd, (void*)&D,
+                             &kc, &vc, (void*)&ctxn };
             hip_launch(d->k_append, cdiv32((u64)B * d->H * (d->hd / 2), 256), 1, 1, 256, 1, 1, 0, args);
         }
         {
-            hipDeviceptr_t qkv = d->qkv, part = d->part;
-            i32 n = (i32)nkeys, chunk = (i32)DEC_CHUNK;
+            hipDeviceptr_t qkv = d->qkv, part = d->part, att = d->att;
             f32 scale = d->scale;
-            void* args[] = { &qkv, (void*)&ldq, &kc, &vc, &n, (void*)&ctxn, (void*)&H, &chunk, &scale, &part };
-            hip_launch(d->k_attn, B * d->H, nsplit, 1, 256, 1, 1, 0, args);
-            i32 ns = (i32)nsplit;
-            hipDeviceptr_t att = d->att;
-            void* args2[] = { &part, &ns, (void*)&H, (void*)&D, &att };
+            void* args[] = { &qkv, (void*)&ldq, &kc, &vc, &posd, (void*)&ctxn, (void*)&H, (void*)&chunk, &scale,
+                             &part };
+            hip_launch(d->k_attn, B * d->H, d->nsplit_max, 1, 256, 1, 1, 0, args);
+            void* args2[] = { &part, &posd, (void*)&chunk, (void*)&nsg, (void*)&H, (void*)&D, &att };
             hip_launch(d->k_merge, B * d->H, 1, 1, 64, 1, 1, 0, args2);
         }
-        /* x2 = x + (att @ Wo + bo) */
-        trlm_gemm_rows(g, GEMM_NN, d->att, trlm_param_ptr(g, trlm_pidx(l, PK_WO)), d->x2, Bi, D, D, D, D, D,
-                       trlm_param_ptr(g, trlm_pidx(l, PK_BO)), d->x);
-        trlm_rmsnorm_rows(g, d->x2, trlm_param_ptr(g, trlm_pidx(l, PK_FFN_NORM)), d->n, d->r, B);
-        trlm_gemm_rows(g, GEMM_NN, d->n, trlm_param_ptr(g, trlm_pidx(l, PK_WGU)), d->gu, Bi, 2 * F, D, D, 2 * F,
-                       2 * F, trlm_param_ptr(g, trlm_pidx(l, PK_BGU)), NULL);
+        /* x2 = x + (att @ Wo + bo); x = x2 + (swiglu(norm(x2) @ Wgu + bgu) @ Wd + bd) */
+        trlm_gemm_rows(g, GEMM_NN, d->att, PP(PK_WO), d->x2, Bi, D, D, D, D, D, PP(PK_BO), d->x);
+        trlm_rmsnorm_rows(g, d->x2, PP(PK_FFN_NORM), d->n, d->r, B);
+        trlm_gemm_rows(g, GEMM_NN, d->n, PP(PK_WGU), d->gu, Bi, 2 * F, D, D, 2 * F, 2 * F, PP(PK_BGU), NULL);
         trlm_swiglu_rows(g, d->gu, d->h, B);
-        /* x = x2 + (h @ Wd + bd) */
-        trlm_gemm_rows(g, GEMM_NN, d->h, trlm_param_ptr(g, trlm_pidx(l, PK_WDOWN)), d->x, Bi, D, F, F, D, D,
-                       trlm_param_ptr(g, trlm_pidx(l, PK_BDOWN)), d->x2);
+        trlm_gemm_rows(g, GEMM_NN, d->h, PP(PK_WDOWN), d->x, Bi, D, F, F, D, D, PP(PK_BDOWN), d->x2);
+#undef PP
     }
     trlm_rmsnorm_rows(g, d->x, trlm_param_ptr(g, trlm_pidx(d->L, 0)), d->nf, d->r, B);
-    head(d);
-    d->len = pos + 1;
+    trlm_gemm_rows(g, GEMM_NT, d->nf, trlm_param_ptr(g, 0), d->logits, Bi, (i32)d->V, D, D, D, (i32)d->ldv, NULL,
+                   NULL);
+    void* args[] = { &posd };
+    hip_launch(d->k_advance, 1, 1, 1, 64, 1, 1, 0, args);
+}
+
+static void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        fprintf(stderr, "[HIP ERROR] gpu_decode: %s -> %s: %s\n", what, hipGetErrorName(e), hipGetErrorString(e));
+        fflush(stderr);
+        _exit(1);
+    }
+}
+
+/* Runs one step: eagerly the first time (the GEMM engine sizes its
+ * workspace), then as a replay of the step captured on the second call. */
+static void run_step(TrlmDecoder* d) {
+    if (d->exec) {
+        check_hip(hipGraphLaunch(d->exec, hip_current_stream()), "hipGraphLaunch");
+    } else if (d->eager_steps == 0) {
+        step_body(d);
+        d->eager_steps++;
+    } else {
+        hipStream_t st = hip_current_stream();
+        check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
+        step_body(d);
+        check_hip(hipStreamEndCapture(st, &d->graph), "hipStreamEndCapture");
+        check_hip(hipGraphInstantiate(&d->exec, d->graph, NULL, NULL, 0), "hipGraphInstantiate");
+        check_hip(hipGraphLaunch(d->exec, st), "hipGraphLaunch");
+    }
+}
+
+void gpu_decoder_step(TrlmDecoder* d, const u32* ids) {
+    if (d->len == 0) dec_fatal("step before prefill");
+    if (d->len >= d->ctx) dec_fatal("context is full (max_ctx reached)");
+    check_tokens(d, ids, d->B);
+    trlm_bind(d->g);
+    hip_h2d(d->ids, ids, (u64)d->B * sizeof(u32));
+    run_step(d);
+    d->len++;
 }
 
 void gpu_decoder_logits(TrlmDecoder* d, f32* host_logits) {
@@ -305,14 +363,24 @@ void gpu_decoder_sample(TrlmDecoder* d, PCGState* rngs, f32 temperature, u32* ou
 }
 
 void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, u32* out) {
+    if (steps == 0) return;
     if ((u64)prompt_len + steps > d->ctx) dec_fatal("prompt_len + steps exceeds max_ctx");
-    u32* cur = (u32*)malloc((u64)d->B * sizeof(u32));
-    if (!cur) dec_fatal("out of host memory");
     gpu_decoder_prefill(d, prompt, prompt_len);
-    for (u32 s = 0; s < steps; s++) {
-        gpu_decoder_greedy(d, cur);
-        for (u32 b = 0; b < d->B; b++) out[(u64)b * steps + s] = cur[b];
-        if (s + 1 < steps) gpu_decoder_step(d, cur);
+    if (d->hist_cap < d->B * steps) {
+        if (d->hist) hip_free(d->hist);
+        d->hist = hip_alloc((u64)d->B * steps * sizeof(u32));
+        d->hist_cap = d->B * steps;
     }
-    free(cur);
+    /* pick s (s = 0 .. steps-1) is taken when *pos_dev = prompt_len + s; it
+     * becomes the ids of the next step directly on the device */
+    hipDeviceptr_t lg = d->logits, ids = d->ids, hist = d->hist, posd = d->pos_dev;
+    i32 ld = (i32)d->ldv, V = (i32)d->V, hl = (i32)steps, base = (i32)prompt_len;
+    void* args[] = { &lg, &ld, &V, &ids, &hist, &hl, &posd, &base };
+    hip_launch(d->k_argmax_hist, d->B, 1, 1, 256, 1, 1, 0, args);
+    for (u32 s = 1; s < steps; s++) {
+        run_step(d);
+        d->len++;
+        hip_launch(d->k_argmax_hist, d->B, 1, 1, 256, 1, 1, 0, args);
+    }
+    hip_d2h(out, d->hist, (u64)d->B * steps * sizeof(u32));
 }

@@ -14,6 +14,8 @@
 //   k_decode_attn_hd*   step: one (sequence, head, context chunk) per block;
 //                       writes the chunk's (max, sum, unnormalised O)
 //   k_decode_merge_hd*  step: combines the chunks in chunk order
+//   k_decode_advance    step: moves the device-resident position on
+//   k_argmax_hist       greedy generation: pick -> next ids and history
 //   k_gather_rows       last prompt row of every sequence
 //   k_sample_rows       sample_next (generate.c:57-73) on the device
 #include "common.h"
@@ -42,13 +44,16 @@ k_cache_fill(const float* __restrict__ qkv, int ldq, int B, int len, int H, int 
 }
 
 // One thread per (sequence b, head h, pair k): rotate q and k of the new
-// token (row b of qkv) by position pos exactly as k_rope_qk does, write q
-// back, append the rotated k and the v pair at cache position pos.
+// token (row b of qkv) by position pos = *pos_dev exactly as k_rope_qk does,
+// write q back, append the rotated k and the v pair at cache position pos.
+// The position lives in device memory so that a captured step replays
+// unchanged (k_decode_advance moves it on).
 extern "C" __global__ void __launch_bounds__(256)
 k_decode_qkv_append(float* __restrict__ qkv, int ldq, const float* __restrict__ cos_t,
-                    const float* __restrict__ sin_t, int pos, int B, int H, int hd, int D, float* __restrict__ kc,
-                    float* __restrict__ vc, int ctx) {
+                    const float* __restrict__ sin_t, const int* __restrict__ pos_dev, int B, int H, int hd, int D,
+                    float* __restrict__ kc, float* __restrict__ vc, int ctx) {
     const int half = hd >> 1;
+    const int pos = *pos_dev;
     int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= B * H * half) return;
     int k = i % half, h = (i / half) % H, b = i / (half * H);
@@ -70,7 +75,7 @@ k_decode_qkv_append(float* __restrict__ qkv, int ldq, const float* __restrict__ 
 
 // grid (B*H, nsplit), 256 threads.  Block (bh, s) covers keys
 // [s*chunk, min((s+1)*chunk, n)) of sequence b, head h, for the query in
-// row b of qkv.  Lanes work in groups of LPR = HD/4 lanes per key row
+// row b of qkv, with n = *pos_dev + 1 (blocks past n write an empty chunk).  Lanes work in groups of LPR = HD/4 lanes per key row
 // (float4 each, so a wave instruction reads whole rows, coalesced);
 // a wave takes every 4th group of RPI = 64/LPR rows.  Output per block:
 // part[(bh*nsplit + s)*(HD + 4) + {0..HD-1, HD, HD+1}] = O (unnormalised),
@@ -78,8 +83,9 @@ k_decode_qkv_append(float* __restrict__ qkv, int ldq, const float* __restrict__ 
 // chunk <= 1024.  Every reduction has a fixed order.
 template <int HD>
 __device__ void decode_attn(const float* __restrict__ qkv, int ldq, const float* __restrict__ kc,
-                            const float* __restrict__ vc, int n, int ctx, int H, int chunk, float scale,
-                            float* __restrict__ part) {
+                            const float* __restrict__ vc, const int* __restrict__ pos_dev, int ctx, int H, int chunk,
+                            float scale, float* __restrict__ part) {
+    const int n = *pos_dev + 1;
     constexpr int LPR = HD / 4, RPI = 64 / LPR;
     __shared__ float sc[1024];
     __shared__ float red[8];
@@ -158,12 +164,15 @@ __device__ void decode_attn(const float* __restrict__ qkv, int ldq, const float*
 }
 
 // One wave per (sequence, head): att[b, h*HD + d] = sum_s w_s O_s[d] /
-// sum_s w_s l_s with w_s = 2^(m_s - max_s m_s), chunks in order.
+// sum_s w_s l_s with w_s = 2^(m_s - max_s m_s), over the chunks that hold
+// keys (n = *pos_dev + 1), in order; records are nsplit_grid per head.
 template <int HD>
-__device__ void decode_merge(const float* __restrict__ part, int nsplit, int H, int D, float* __restrict__ att) {
+__device__ void decode_merge(const float* __restrict__ part, const int* __restrict__ pos_dev, int chunk,
+                             int nsplit_grid, int H, int D, float* __restrict__ att) {
     const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
     const int d = threadIdx.x;
-    const float* p = part + (long long)bh * nsplit * (HD + 4);
+    const int nsplit = (*pos_dev + chunk) / chunk;
+    const float* p = part + (long long)bh * nsplit_grid * (HD + 4);
     float M = -INFINITY;
     for (int s = 0; s < nsplit; s++) M = fmaxf(M, p[s * (HD + 4) + HD]);
     float L = 0.f, o = 0.f;
@@ -178,18 +187,58 @@ __device__ void decode_merge(const float* __restrict__ part, int nsplit, int H, 
 
 #define DECODE_KERNELS(HD)                                                                                  \
     extern "C" __global__ void __launch_bounds__(256)                                                       \
-    k_decode_attn_hd##HD(const float* qkv, int ldq, const float* kc, const float* vc, int n, int ctx, int H, \
-                         int chunk, float scale, float* part) {                                             \
-        decode_attn<HD>(qkv, ldq, kc, vc, n, ctx, H, chunk, scale, part);                                   \
+    k_decode_attn_hd##HD(const float* qkv, int ldq, const float* kc, const float* vc, const int* pos_dev,   \
+                         int ctx, int H, int chunk, float scale, float* part) {                             \
+        decode_attn<HD>(qkv, ldq, kc, vc, pos_dev, ctx, H, chunk, scale, part);                             \
     }                                                                                                       \
     extern "C" __global__ void __launch_bounds__(64)                                                        \
-    k_decode_merge_hd##HD(const float* part, int nsplit, int H, int D, float* att) {                        \
-        decode_merge<HD>(part, nsplit, H, D, att);                                                          \
+    k_decode_merge_hd##HD(const float* part, const int* pos_dev, int chunk, int nsplit_grid, int H, int D,  \
+                          float* att) {                                                                     \
+        decode_merge<HD>(part, pos_dev, chunk, nsplit_grid, H, D, att);                                     \
     }
 
 DECODE_KERNELS(16)
 DECODE_KERNELS(32)
 DECODE_KERNELS(64)
+
+// *pos_dev += 1: the step's token is in the cache.
+extern "C" __global__ void k_decode_advance(int* __restrict__ pos_dev) {
+    if (threadIdx.x == 0 && blockIdx.x == 0) *pos_dev = *pos_dev + 1;
+}
+
+// Greedy pick per row (first index of the maximum, as k_argmax_rows), written
+// both as the next step's input ids[row] and into hist[row*hist_ld + step]
+// with step = *pos_dev - pos_base, so generation needs no host round trip.
+extern "C" __global__ void __launch_bounds__(256)
+k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restrict__ ids,
+              unsigned* __restrict__ hist, int hist_ld, const int* __restrict__ pos_dev, int pos_base) {
+    __shared__ float bv[4];
+    __shared__ int bi[4];
+    const float* z = logits + (long long)blockIdx.x * ld;
+    float best = -INFINITY;
+    int idx = 0x7fffffff;
+    for (int j = threadIdx.x; j < V; j += 256) {
+        float v = z[j];
+        if (v > best) { best = v; idx = j; }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        float v2 = __shfl_xor(best, o, WAVE);
+        int i2 = __shfl_xor(idx, o, WAVE);
+        if (v2 > best || (v2 == best && i2 < idx)) { best = v2; idx = i2; }
+    }
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    if (lane == 0) { bv[wave] = best; bi[wave] = idx; }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float b = bv[0];
+        int k = bi[0];
+        for (int w = 1; w < 4; w++)
+            if (bv[w] > b || (bv[w] == b && bi[w] < k)) { b = bv[w]; k = bi[w]; }
+        ids[blockIdx.x] = (unsigned)k;
+        hist[(long long)blockIdx.x * hist_ld + (*pos_dev - pos_base)] = (unsigned)k;
+    }
+}
 
 // dst[i, :] = src[(i*stride + offset), :]  (cols floats per row)
 extern "C" __global__ void __launch_bounds__(256)

@@ -267,7 +267,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     if (full) gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, ALIGNED>(p, A, B, m0, n0, kb, ke, lds, acc);
     else gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, false>(p, A, B, m0, n0, kb, ke, lds, acc);
 
-    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.
+    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.  C and
+    // resid values are loaded four rows at a time before the four stores:
+    // the compiler cannot prove that C aliases neither, so a load after a
+    // store would otherwise wait for the one before it.
     const int half = lane >> 5, col_l = lane & 31;
 #pragma unroll
     for (int i = 0; i < FM; i++)
@@ -277,15 +280,25 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
             if (col >= p.N) continue;
             const float bv = p.bias ? p.bias[col] : 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int row = m0 + wm0 + i * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                if (row < p.M) {
-                    float v = p.alpha * acc[i][j][r];
-                    float* dst = C + (long long)row * p.ldc + col;
-                    if (p.beta != 0.f) v = v + p.beta * *dst;
-                    if (p.bias) v = v + bv;
-                    if (p.resid) v = p.resid[(long long)row * p.ldr + col] + v;
-                    *dst = v;
+            for (int g = 0; g < 4; g++) {
+                float cv[4], rv[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int row = m0 + wm0 + i * 32 + 8 * g + 4 * half + q;
+                    const bool ok = row < p.M;
+                    cv[q] = (ok && p.beta != 0.f) ? C[(long long)row * p.ldc + col] : 0.f;
+                    rv[q] = (ok && p.resid) ? p.resid[(long long)row * p.ldr + col] : 0.f;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int row = m0 + wm0 + i * 32 + 8 * g + 4 * half + q;
+                    if (row < p.M) {
+                        float v = p.alpha * acc[i][j][4 * g + q];
+                        if (p.beta != 0.f) v = v + p.beta * cv[q];
+                        if (p.bias) v = v + bv;
+                        if (p.resid) v = rv[q] + v;
+                        C[(long long)row * p.ldc + col] = v;
+                    }
                 }
             }
         }
