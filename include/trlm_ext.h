@@ -61,6 +61,18 @@ const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 ba
  * Returns 0, or -1 for an unknown name (selection is then automatic). */
 i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits);
 
+/* ---- checkpoints: TRLM v1 (training/checkpoint.h:6-12), the reference's
+ * format and rules (checkpoint.c:22-137), straight from / to the device.
+ * save: shapes from params (the caller's CPU mirror nodes), values and, when
+ * opt != NULL, Adam m / v from the device, t from opt; written to
+ * path ".tmp" and renamed over path only when complete.  load: validates
+ * the whole file against params (count, ndim, shapes, exact size; optimizer
+ * state required when opt != NULL) and changes nothing on failure; on
+ * success fills the device buffers, the host mirror params[i]->value and, when
+ * opt != NULL, opt->m / opt->v / opt->t.  Both return TRUE / FALSE. */
+bool32 gpu_trainer_checkpoint_save(GpuTrainer* g, const char* path, Node** params, const AdamOptimizer* opt);
+bool32 gpu_trainer_checkpoint_load(GpuTrainer* g, const char* path, Node** params, AdamOptimizer* opt);
+
 /* ---- KV-cache decode (generate.c:57-73,186-212 without the per-step
  * full-window recompute).  The decoder uses the trainer's resident
  * parameters, kernels, stream and GEMM engine; it owns a K/V cache of

@@ -172,6 +172,84 @@ def pcg_stream(seed_a, seed_b):
     return r
 
 
+# ---- checkpoint TRLM v1 (training/checkpoint.h:6-12, checkpoint.c:22-137) ----
+# [4 B "TRLM"][u32 version=1][u32 num_params][u32 has_opt]
+# per parameter: [u32 ndim][ndim x u64 shape][numel x f32]
+# if has_opt: per parameter [numel x f32 m][numel x f32 v], then [u64 t]
+# Little-endian, as written by the x86-64 reference.
+
+def trlm_bytes(shapes, params, m=None, v=None, t=0):
+    """The bytes checkpoint_save writes for these flat buffers."""
+    import struct
+    has_opt = m is not None
+    out = [b"TRLM", struct.pack("<III", 1, len(shapes), 1 if has_opt else 0)]
+    off = 0
+    p = np.ascontiguousarray(params, np.float32)
+    for sh in shapes:
+        n = int(np.prod(sh))
+        out.append(struct.pack("<I", len(sh)) + struct.pack("<%dQ" % len(sh), *sh))
+        out.append(p[off:off + n].tobytes())
+        off += n
+    if has_opt:
+        mm, vv = np.ascontiguousarray(m, np.float32), np.ascontiguousarray(v, np.float32)
+        off = 0
+        for sh in shapes:
+            n = int(np.prod(sh))
+            out.append(mm[off:off + n].tobytes())
+            out.append(vv[off:off + n].tobytes())
+            off += n
+        out.append(struct.pack("<Q", t))
+    return b"".join(out)
+
+
+def trlm_parse(data, shapes, want_opt):
+    """checkpoint_load's validation and copy: (params, m, v, t) or None when
+    the reference would return FALSE (bad magic/version/count, a shape that
+    differs, a size that is not exactly the expected one, optimizer state
+    asked for but absent)."""
+    import struct
+    if len(data) < 16 or data[:4] != b"TRLM":
+        return None
+    version, num, has_opt = struct.unpack_from("<III", data, 4)
+    if version != 1 or num != len(shapes) or (want_opt and not has_opt):
+        return None
+    pos = 16
+    offs = []
+    total = 0
+    for sh in shapes:
+        if pos + 4 > len(data):
+            return None
+        nd = struct.unpack_from("<I", data, pos)[0]
+        pos += 4
+        if nd != len(sh):
+            return None
+        for d in sh:
+            if pos + 8 > len(data) or struct.unpack_from("<Q", data, pos)[0] != d:
+                return None
+            pos += 8
+        n = int(np.prod(sh))
+        if pos + 4 * n > len(data):
+            return None
+        offs.append((pos, n))
+        pos += 4 * n
+        total += n
+    opt_at = pos
+    if has_opt:
+        pos += 8 * total + 8
+    if pos != len(data):
+        return None
+    params = np.concatenate([np.frombuffer(data, np.float32, n, o) for o, n in offs])
+    if not want_opt:
+        return params, None, None, None
+    m, v = [], []
+    pos = opt_at
+    for _, n in offs:
+        m.append(np.frombuffer(data, np.float32, n, pos)); pos += 4 * n
+        v.append(np.frombuffer(data, np.float32, n, pos)); pos += 4 * n
+    t = struct.unpack_from("<Q", data, pos)[0]
+    return params, np.concatenate(m), np.concatenate(v), t
+
+
 def sample_next(row, temperature, pcg):
     """sample_next on one row of logits; pcg (a Pcg) advances by one draw."""
     row = np.ascontiguousarray(row, np.float32)
@@ -236,6 +314,14 @@ class Reference:
         h.refh_time_forward.restype = C.c_double
         h.refh_time_forward.argtypes = [cfgp, f32p, u32p, C.c_uint32, C.c_uint32, f32p, C.c_int]
         h.refh_time_matmul.restype = C.c_double
+        h.refh_checkpoint_save.restype = C.c_int
+        h.refh_checkpoint_save.argtypes = [C.POINTER(RefCfg), f32p, C.c_void_p, C.c_void_p, C.c_uint64, C.c_int,
+                                           C.c_char_p]
+        h.refh_checkpoint_save_init.restype = C.c_int
+        h.refh_checkpoint_save_init.argtypes = [C.POINTER(RefCfg), C.c_uint64, C.c_uint64, C.c_char_p]
+        h.refh_checkpoint_load.restype = C.c_int
+        h.refh_checkpoint_load.argtypes = [C.POINTER(RefCfg), C.c_char_p, f32p, C.c_void_p, C.c_void_p,
+                                           C.POINTER(C.c_uint64), C.c_int]
         h.refh_time_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
 
     def lm_init(self, model, seed_a=1337, seed_b=1):
@@ -259,6 +345,29 @@ class Reference:
 
     def adam_step(self, model, p, g, m, v, t_before, lr, b1, b2, eps):
         self.h.refh_adam_step(C.byref(model.cfg), p, g, m, v, t_before, lr, b1, b2, eps)
+
+    def checkpoint_save(self, model, path, params, m=None, v=None, t=0):
+        c = RefCfg(model.V, model.D, model.H, model.L, model.F, model.eps)
+        has = m is not None
+        mm = np.ascontiguousarray(m, np.float32) if has else None
+        vv = np.ascontiguousarray(v, np.float32) if has else None
+        return bool(self.h.refh_checkpoint_save(C.byref(c), np.ascontiguousarray(params, np.float32),
+                                                mm.ctypes.data if has else None, vv.ctypes.data if has else None,
+                                                t, int(has), path.encode()))
+
+    def checkpoint_save_init(self, model, path, seed_a=1337, seed_b=1):
+        c = RefCfg(model.V, model.D, model.H, model.L, model.F, model.eps)
+        return bool(self.h.refh_checkpoint_save_init(C.byref(c), seed_a, seed_b, path.encode()))
+
+    def checkpoint_load(self, model, path, total, want_opt):
+        c = RefCfg(model.V, model.D, model.H, model.L, model.F, model.eps)
+        p = np.zeros(total, np.float32)
+        m = np.zeros(total, np.float32) if want_opt else None
+        v = np.zeros(total, np.float32) if want_opt else None
+        t = C.c_uint64(0)
+        ok = self.h.refh_checkpoint_load(C.byref(c), path.encode(), p, m.ctypes.data if want_opt else None,
+                                         v.ctypes.data if want_opt else None, C.byref(t), int(want_opt))
+        return (p, m, v, t.value) if ok else None
 
     def matmul(self, A, B):
         A = np.ascontiguousarray(A, np.float32)

@@ -29,6 +29,7 @@
 #include "model/rope.h"
 #include "model/loss.h"
 #include "training/adam.h"
+#include "training/checkpoint.h"
 
 static struct {
     Allocator (*allocator_create)(u64);
@@ -54,6 +55,8 @@ static struct {
     f64 (*m_sin)(f64); f64 (*m_cos)(f64);
     f32 (*m_powf)(f32, f32); f32 (*m_expf)(f32); f32 (*m_logf)(f32); f32 (*m_sqrtf)(f32);
     f32 (*m_sinf)(f32); f32 (*m_cosf)(f32);
+    bool32 (*checkpoint_save)(const char*, Node**, u32, const AdamOptimizer*);
+    bool32 (*checkpoint_load)(Allocator*, const char*, Node**, u32, AdamOptimizer*);
     int ok;
 } R;
 
@@ -70,6 +73,7 @@ int refh_open(const char* lib_path) {
     LOAD(backward); LOAD(adam_create); LOAD(adam_step); LOAD(adam_step_parallel);
     LOAD(m_sqrt); LOAD(m_exp); LOAD(m_log); LOAD(m_pow); LOAD(m_sin); LOAD(m_cos);
     LOAD(m_powf); LOAD(m_expf); LOAD(m_logf); LOAD(m_sqrtf); LOAD(m_sinf); LOAD(m_cosf);
+    LOAD(checkpoint_save); LOAD(checkpoint_load);
     R.ok = 1;
     return 0;
 }
@@ -333,4 +337,71 @@ double refh_time_matmul(u32 M, u32 N, u32 K, const f32* A, const f32* B, f32* C)
     double t0 = now_s();
     refh_matmul(M, N, K, A, B, C);
     return now_s() - t0;
+}
+
+/* ---- checkpoint TRLM v1 (training/checkpoint.c) over flat buffers ---- */
+
+/* checkpoint_save of the model whose parameters are `params` (flat, in
+ * lm_collect_params order) and, when has_opt, Adam state m, v, t. */
+int refh_checkpoint_save(const RefCfg* c, const f32* params, const f32* m, const f32* v, u64 t, int has_opt,
+                         const char* path) {
+    Allocator a = R.allocator_create(arena_for(c, 1));
+    Node* ps[LM_MAX_LAYERS * 12 + 2];
+    u32 np;
+    model_from_flat(&a, c, params, ps, &np);
+    AdamOptimizer opt = R.adam_create(&a, ps, np, 3e-4f, 0.9f, 0.95f, 1e-8f);
+    opt.t = t;
+    if (has_opt) {
+        u64 off = 0;
+        for (u32 i = 0; i < np; i++) {
+            u64 n = ps[i]->value.numel;
+            memcpy(opt.m[i].data, m + off, n * sizeof(f32));
+            memcpy(opt.v[i].data, v + off, n * sizeof(f32));
+            off += n;
+        }
+    }
+    int ok = (int)R.checkpoint_save(path, ps, np, has_opt ? &opt : NULL);
+    R.allocator_destroy(&a);
+    return ok;
+}
+
+/* checkpoint_load into flat buffers (params always; m, v, *t when want_opt).
+ * Returns the reference's result; on failure nothing is written. */
+int refh_checkpoint_load(const RefCfg* c, const char* path, f32* params, f32* m, f32* v, u64* t, int want_opt) {
+    Allocator a = R.allocator_create(arena_for(c, 1));
+    Allocator scratch = R.allocator_create(4 * arena_for(c, 1));
+    Node* ps[LM_MAX_LAYERS * 12 + 2];
+    u32 np;
+    model_from_flat(&a, c, params, ps, &np);
+    AdamOptimizer opt = R.adam_create(&a, ps, np, 3e-4f, 0.9f, 0.95f, 1e-8f);
+    int ok = (int)R.checkpoint_load(&scratch, path, ps, np, want_opt ? &opt : NULL);
+    if (ok) {
+        u64 off = 0;
+        for (u32 i = 0; i < np; i++) {
+            u64 n = ps[i]->value.numel;
+            memcpy(params + off, ps[i]->value.data, n * sizeof(f32));
+            if (want_opt) {
+                memcpy(m + off, opt.m[i].data, n * sizeof(f32));
+                memcpy(v + off, opt.v[i].data, n * sizeof(f32));
+            }
+            off += n;
+        }
+        if (want_opt) *t = opt.t;
+    }
+    R.allocator_destroy(&scratch);
+    R.allocator_destroy(&a);
+    return ok;
+}
+
+/* checkpoint_save of a model built by the reference's own lm_init (so the
+ * file's shapes are lm_init's), without optimizer state. */
+int refh_checkpoint_save_init(const RefCfg* c, u64 sa, u64 sb, const char* path) {
+    Allocator a = R.allocator_create(arena_for(c, 1));
+    PCGState rng = R.pcg_seed(sa, sb);
+    LMModel m = R.lm_init(&a, &rng, c->V, c->D, c->H, c->L, c->F, c->eps);
+    Node* ps[LM_MAX_LAYERS * 12 + 2];
+    u32 np = R.lm_collect_params(&m, ps);
+    int ok = (int)R.checkpoint_save(path, ps, np, NULL);
+    R.allocator_destroy(&a);
+    return ok;
 }

@@ -275,3 +275,72 @@ def test_sample_next_closed_forms(orc):
         assert got == (0 if e0 >= u * (e0 + e1) else 1)
         picks.append(got)
     assert 0 < sum(picks) < 200
+
+
+def _ref_or_skip(orc):
+    if not orc.reference_available():
+        pytest.skip("oracle/_ref was not built (no /root/reference here)")
+    return orc.Reference()
+
+
+def test_checkpoint_format_matches_reference(orc, tmp_path):
+    """The oracle's TRLM v1 restatement (checkpoint.h:6-12) writes the bytes
+    the reference's checkpoint_save writes -- for a model built by the
+    reference's own lm_init (so shapes are lm_init's), and for flat buffers
+    with optimizer state -- and reads back exactly what checkpoint_load
+    reads."""
+    ref = _ref_or_skip(orc)
+    model = orc.Model(61, 32, 2, 2, 48)
+    params = model.init(1337, 1)
+    p1 = str(tmp_path / "init.trlm")
+    assert ref.checkpoint_save_init(model, p1, 1337, 1)
+    assert open(p1, "rb").read() == orc.trlm_bytes(model.shapes(), params)
+    rng = np.random.default_rng(3)
+    m = rng.standard_normal(params.size).astype(np.float32)
+    v = rng.random(params.size).astype(np.float32)
+    p2 = str(tmp_path / "opt.trlm")
+    assert ref.checkpoint_save(model, p2, params, m, v, 123456789012)
+    data = open(p2, "rb").read()
+    assert data == orc.trlm_bytes(model.shapes(), params, m, v, 123456789012)
+    got = ref.checkpoint_load(model, p2, params.size, True)
+    mine = orc.trlm_parse(data, model.shapes(), True)
+    for a, b in zip(got[:3], mine[:3]):
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    assert got[3] == mine[3] == 123456789012
+
+
+@pytest.mark.parametrize("case", ["truncated", "magic", "version", "count", "shape", "no_opt", "trailing"])
+def test_checkpoint_rejections_match_reference(orc, tmp_path, case):
+    """checkpoint_load's FALSE cases (checkpoint.c:75-125): the oracle's
+    parser rejects exactly the files the reference rejects."""
+    import struct
+    ref = _ref_or_skip(orc)
+    model = orc.Model(53, 32, 2, 1, 32)
+    params = model.init(7, 1)
+    rng = np.random.default_rng(5)
+    m, v = rng.standard_normal((2, params.size)).astype(np.float32)
+    good = orc.trlm_bytes(model.shapes(), params, m, v, 9)
+    want_opt = True
+    if case == "truncated":
+        data = good[:-5]
+    elif case == "magic":
+        data = b"TRLX" + good[4:]
+    elif case == "version":
+        data = good[:4] + struct.pack("<I", 2) + good[8:]
+    elif case == "count":
+        data = good[:8] + struct.pack("<I", len(model.shapes()) + 1) + good[12:]
+    elif case == "shape":
+        data = good[:20] + struct.pack("<Q", model.V + 1) + good[28:]
+    elif case == "no_opt":
+        data = orc.trlm_bytes(model.shapes(), params)
+    else:
+        data = good + b"\0"
+    path = str(tmp_path / ("bad_%s.trlm" % case))
+    open(path, "wb").write(data)
+    assert ref.checkpoint_load(model, path, params.size, want_opt) is None
+    assert orc.trlm_parse(data, model.shapes(), want_opt) is None
+    # the unmodified file loads in both
+    ok = str(tmp_path / "good.trlm")
+    open(ok, "wb").write(good)
+    assert ref.checkpoint_load(model, ok, params.size, want_opt) is not None
+    assert orc.trlm_parse(good, model.shapes(), want_opt) is not None

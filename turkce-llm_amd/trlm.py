@@ -163,6 +163,9 @@ def _bind(host, hip):
     _sig(hip, "gpu_trainer_forward_logits", None, [GP, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_forward_loss_logits", C.c_float, [GP, u32p, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_greedy_argmax", None, [GP, u32p])
+    ckpt_args = [GP, C.c_char_p, C.POINTER(NodeP), C.POINTER(AdamOptimizer)]
+    _sig(hip, "gpu_trainer_checkpoint_save", C.c_uint32, ckpt_args)
+    _sig(hip, "gpu_trainer_checkpoint_load", C.c_uint32, ckpt_args)
     DP = C.c_void_p
     f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
     _sig(hip, "gpu_decoder_create", DP, [GP, C.c_uint32, C.c_uint32])
@@ -373,6 +376,14 @@ class Trainer:
 
     def adamw_step(self, adam, wd, scale=1.0):
         self.hip.gpu_trainer_adamw_step_scaled(C.byref(self.g), C.byref(adam.opt), wd, scale)
+
+    def checkpoint_save(self, path, adam=None):
+        return bool(self.hip.gpu_trainer_checkpoint_save(C.byref(self.g), path.encode(), self.hm.nodes,
+                                                         C.byref(adam.opt) if adam else None))
+
+    def checkpoint_load(self, path, adam=None):
+        return bool(self.hip.gpu_trainer_checkpoint_load(C.byref(self.g), path.encode(), self.hm.nodes,
+                                                         C.byref(adam.opt) if adam else None))
 
     def forward_logits(self, ids):
         out = np.zeros((self.B * self.T, self.hm.V), np.float32)
