@@ -58,6 +58,13 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
               bias, resid, ldc);
 }
 
+/* threads of k_swiglu_fwd / k_swiglu_bwd: one float4 each when F % 4 == 0 */
+static u32 swiglu_blocks(const GpuTrainer* g, u64 rows) {
+    u64 work = rows * g->F;
+    if (g->F % 4 == 0) work /= 4;
+    return cdiv_u64(work, 256);
+}
+
 static void rmsnorm_rows(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv,
                          u32 nrows) {
     i32 rows = (i32)nrows, cols = (i32)g->D;
@@ -126,7 +133,7 @@ static void rope(GpuTrainer* g, hipDeviceptr_t qkv, i32 inverse) {
     hipDeviceptr_t c = g->cos_t, s = g->sin_t;
     i32 N = (i32)g->N, T = (i32)g->T, H = (i32)g->H, hd = (i32)g->hd, ld = 3 * (i32)g->D;
     void* args[] = { &qkv, &c, &s, &N, &T, &H, &hd, &ld, &inverse };
-    hip_launch(g->k.rope_qk, cdiv_u64((u64)g->N * g->H * (g->hd / 2), 256), 1, 1, 256, 1, 1, 0, args);
+    hip_launch(g->k.rope_qk, cdiv_u64((u64)g->N * g->H * (g->hd / 4), 256), 1, 1, 256, 1, 1, 0, args);
 }
 
 /* ---------------- create / destroy ---------------- */
@@ -388,7 +395,7 @@ void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void
         {
             hipDeviceptr_t gu = a->gu, h = a->h;
             void* args[] = { &gu, &h, &N, &F };
-            hip_launch(g->k.swiglu_fwd, cdiv_u64((u64)N * F, 256), 1, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.swiglu_fwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);
         }
         /* x_out = x2 + (h @ Wd + bd) */
         gemm1(g, GEMM_NN, a->h, P_(g, pidx(l, PK_WDOWN)), x_out, N, D, F, F, D, D, 0.0f, P_(g, pidx(l, PK_BDOWN)),
@@ -438,7 +445,7 @@ static void backward_pass(GpuTrainer* g) {
         {
             hipDeviceptr_t gu = a->gu, dh = g->dh, dgu = g->dgu;
             void* args[] = { &gu, &dh, &dgu, &N, &F };
-            hip_launch(g->k.swiglu_bwd, cdiv_u64((u64)N * F, 256), 1, 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.swiglu_bwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);
         }
         gemm1(g, GEMM_TN, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), D, 2 * F, N, D, 2 * F, 2 * F, 0.0f, NULL, NULL);
         colsum(g, g->dgu, G_(g, pidx(ul, PK_BGU)), N, 2 * F);
@@ -594,7 +601,7 @@ void trlm_gemm_rows(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr
 void trlm_swiglu_rows(GpuTrainer* g, hipDeviceptr_t gu, hipDeviceptr_t h, u32 rows) {
     i32 n = (i32)rows, F = (i32)g->F;
     void* args[] = { &gu, &h, &n, &F };
-    hip_launch(g->k.swiglu_fwd, cdiv_u64((u64)rows * g->F, 256), 1, 1, 256, 1, 1, 0, args);
+    hip_launch(g->k.swiglu_fwd, swiglu_blocks(g, rows), 1, 1, 256, 1, 1, 0, args);
 }
 
 void trlm_embed_rows(GpuTrainer* g, hipDeviceptr_t ids, hipDeviceptr_t x, u32 rows) {

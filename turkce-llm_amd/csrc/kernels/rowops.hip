@@ -62,13 +62,40 @@ k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w, float* _
     int lane = threadIdx.x & 63;
     if (row >= rows) return;
     const float* xr = x + (long long)row * cols;
+    float* orow = out + (long long)row * cols;
+    if ((cols & 3) == 0 && cols <= 1024) {
+        // the row in registers: float4 chunks q = lane + 64*i
+        const int c4 = cols >> 2;
+        f32x4 v[4];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = lane + 64 * i;
+            v[i] = q < c4 ? *(const f32x4*)(xr + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+            ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+        }
+        ss = wave_sum(ss);
+        float r = 1.0f / (float)sqrt((double)(ss / (float)cols + eps));
+        if (lane == 0) rinv[row] = r;
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = lane + 64 * i;
+            if (q < c4) {
+                f32x4 wv = *(const f32x4*)(w + 4 * q);
+                f32x4 o;
+#pragma unroll
+                for (int e = 0; e < 4; e++) o[e] = v[i][e] * r * wv[e];
+                *(f32x4*)(orow + 4 * q) = o;
+            }
+        }
+        return;
+    }
     float ss = 0.f;
     for (int i = lane; i < cols; i += 64) ss += xr[i] * xr[i];
     ss = wave_sum(ss);
     float ms = ss / (float)cols;
     float r = 1.0f / (float)sqrt((double)(ms + eps));
     if (lane == 0) rinv[row] = r;
-    float* orow = out + (long long)row * cols;
     for (int i = lane; i < cols; i += 64) orow[i] = xr[i] * r * w[i];
 }
 
@@ -84,23 +111,77 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * RMS_ROWS;
     float* mine = part + wave * cols;
-    for (int i = lane; i < cols; i += 64) mine[i] = 0.f;
     // wave `wave` handles rows r0 + wave*RMS_ROWS/4 .. in order
-    for (int rr = 0; rr < RMS_ROWS / 4; rr++) {
-        int row = r0 + wave * (RMS_ROWS / 4) + rr;
-        if (row >= rows) break;
-        const float* xr = x + (long long)row * cols;
-        const float* d = dy + (long long)row * cols;
-        float* g = dx + (long long)row * cols;
-        float r = rinv[row];
-        float r3 = r * r * r;
-        float S = 0.f;
-        for (int i = lane; i < cols; i += 64) S += d[i] * w[i] * xr[i];
-        S = wave_sum(S);
-        float c = r3 / (float)cols;
-        for (int j = lane; j < cols; j += 64) {
-            g[j] += w[j] * r * d[j] - c * xr[j] * S;
-            mine[j] += d[j] * xr[j] * r;
+    if ((cols & 3) == 0 && cols <= 1024) {
+        // rows in registers, float4 chunks q = lane + 64*i; the dy*x*r
+        // partial of the wave's rows accumulates in registers in row order
+        const int c4 = cols >> 2;
+        f32x4 wv[4], acc[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = lane + 64 * i;
+            wv[i] = q < c4 ? *(const f32x4*)(w + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+            acc[i] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int rr = 0; rr < RMS_ROWS / 4; rr++) {
+            const int row = r0 + wave * (RMS_ROWS / 4) + rr;
+            if (row >= rows) break;
+            const float* xr = x + (long long)row * cols;
+            const float* d = dy + (long long)row * cols;
+            float* g = dx + (long long)row * cols;
+            f32x4 xv[4], dv[4], gv[4];
+            float S = 0.f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = lane + 64 * i;
+                const bool ok = q < c4;
+                xv[i] = ok ? *(const f32x4*)(xr + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+                dv[i] = ok ? *(const f32x4*)(d + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+                gv[i] = ok ? *(const f32x4*)(g + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int e = 0; e < 4; e++) S += dv[i][e] * wv[i][e] * xv[i][e];
+            }
+            S = wave_sum(S);
+            const float r = rinv[row];
+            const float c = r * r * r / (float)cols;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int q = lane + 64 * i;
+                if (q < c4) {
+                    f32x4 o;
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        o[e] = gv[i][e] + (wv[i][e] * r * dv[i][e] - c * xv[i][e] * S);
+                        acc[i][e] += dv[i][e] * xv[i][e] * r;
+                    }
+                    *(f32x4*)(g + 4 * q) = o;
+                }
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int q = lane + 64 * i;
+            if (q < c4) *(f32x4*)(mine + 4 * q) = acc[i];
+        }
+    } else {
+        for (int i = lane; i < cols; i += 64) mine[i] = 0.f;
+        for (int rr = 0; rr < RMS_ROWS / 4; rr++) {
+            int row = r0 + wave * (RMS_ROWS / 4) + rr;
+            if (row >= rows) break;
+            const float* xr = x + (long long)row * cols;
+            const float* d = dy + (long long)row * cols;
+            float* g = dx + (long long)row * cols;
+            float r = rinv[row];
+            float r3 = r * r * r;
+            float S = 0.f;
+            for (int i = lane; i < cols; i += 64) S += d[i] * w[i] * xr[i];
+            S = wave_sum(S);
+            float c = r3 / (float)cols;
+            for (int j = lane; j < cols; j += 64) {
+                g[j] += w[j] * r * d[j] - c * xr[j] * S;
+                mine[j] += d[j] * xr[j] * r;
+            }
         }
     }
     __syncthreads();
@@ -198,24 +279,33 @@ k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __res
 extern "C" __global__ void __launch_bounds__(256)
 k_rope_qk(float* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int N, int T,
           int H, int hd, int ld, int inverse) {
-    int half = hd >> 1, D = H * hd;
-    long long total = (long long)N * H * half;
+    // one thread per (row n, head h, pair group k2): pairs 2*k2 and 2*k2+1,
+    // i.e. the float4 at columns h*hd + 4*k2 of the Q part and of the K part
+    const int half = hd >> 1, q4 = hd >> 2, D = H * hd;
+    long long total = (long long)N * H * q4;
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= total) return;
-    int k = (int)(i % half);
-    long long rest = i / half;
+    int k2 = (int)(i % q4);
+    long long rest = i / q4;
     int h = (int)(rest % H);
     long long n = rest / H;
     int t = (int)(n % T);
-    float c = cos_t[t * half + k], s = sin_t[t * half + k];
-    float* row = qkv + n * (long long)ld;
-    int c0 = h * hd + 2 * k;
+    const int k = 2 * k2;
+    const float c0 = cos_t[t * half + k], s0 = sin_t[t * half + k];
+    const float c1 = cos_t[t * half + k + 1], s1 = sin_t[t * half + k + 1];
+    float* row = qkv + n * (long long)ld + h * hd + 4 * k2;
 #pragma unroll
     for (int part = 0; part < 2; part++) {
-        float* p = row + part * D + c0;
-        float a0 = p[0], a1 = p[1];
-        if (!inverse) { p[0] = a0 * c - a1 * s; p[1] = a0 * s + a1 * c; }
-        else { p[0] = a0 * c + a1 * s; p[1] = -a0 * s + a1 * c; }
+        f32x4 a = *(f32x4*)(row + part * D);
+        f32x4 o;
+        if (!inverse) {
+            o[0] = a[0] * c0 - a[1] * s0; o[1] = a[0] * s0 + a[1] * c0;
+            o[2] = a[2] * c1 - a[3] * s1; o[3] = a[2] * s1 + a[3] * c1;
+        } else {
+            o[0] = a[0] * c0 + a[1] * s0; o[1] = -a[0] * s0 + a[1] * c0;
+            o[2] = a[2] * c1 + a[3] * s1; o[3] = -a[2] * s1 + a[3] * c1;
+        }
+        *(f32x4*)(row + part * D) = o;
     }
 }
 
@@ -224,6 +314,21 @@ k_rope_qk(float* __restrict__ qkv, const float* __restrict__ cos_t, const float*
 extern "C" __global__ void __launch_bounds__(256)
 k_swiglu_fwd(const float* __restrict__ gu, float* __restrict__ h, int rows, int F) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((F & 3) == 0) {   // one float4 of h per thread
+        const int q = F >> 2;
+        if (i >= (long long)rows * q) return;
+        long long n = i / q;
+        int j = (int)(i - n * q) * 4;
+        f32x4 g = *(const f32x4*)(gu + n * 2 * F + j), u = *(const f32x4*)(gu + n * 2 * F + F + j);
+        f32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float sg = 1.0f / (1.0f + expf(-g[e]));
+            o[e] = (g[e] * sg) * u[e];
+        }
+        *(f32x4*)(h + n * F + j) = o;
+        return;
+    }
     if (i >= (long long)rows * F) return;
     long long n = i / F;
     int j = (int)(i - n * F);
@@ -237,6 +342,25 @@ k_swiglu_fwd(const float* __restrict__ gu, float* __restrict__ h, int rows, int 
 extern "C" __global__ void __launch_bounds__(256)
 k_swiglu_bwd(const float* __restrict__ gu, const float* __restrict__ dh, float* __restrict__ dgu, int rows, int F) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if ((F & 3) == 0) {   // one float4 of dh per thread
+        const int q = F >> 2;
+        if (i >= (long long)rows * q) return;
+        long long n = i / q;
+        int j = (int)(i - n * q) * 4;
+        f32x4 g = *(const f32x4*)(gu + n * 2 * F + j), u = *(const f32x4*)(gu + n * 2 * F + F + j);
+        f32x4 d = *(const f32x4*)(dh + n * F + j);
+        f32x4 dg, du;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            float sg = 1.0f / (1.0f + expf(-g[e]));
+            float silu_g = d[e] * u[e];
+            dg[e] = silu_g * sg + (silu_g * g[e]) * (sg * (1.0f - sg));
+            du[e] = d[e] * (g[e] * sg);
+        }
+        *(f32x4*)(dgu + n * 2 * F + j) = dg;
+        *(f32x4*)(dgu + n * 2 * F + F + j) = du;
+        return;
+    }
     if (i >= (long long)rows * F) return;
     long long n = i / F;
     int j = (int)(i - n * F);
