@@ -301,7 +301,85 @@ def tune(trlm, hip, reps, out_path=None):
     dev.close()
 
 
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "lm_head_fwd_hbm_traffic.txt")
+PROBE_COPY_BYTES = 512 << 20
+
+
+def traffic_probe(trlm):
+    """Dispatches for the HBM-traffic counter passes: three device copies of
+    PROBE_COPY_BYTES (the calibration: a plain copy reads and writes exactly
+    that many bytes), then three LM-head forward GEMMs of the sweep."""
+    _, hip = trlm.libs()
+    rt = C.CDLL("libamdhip64.so")
+    rt.hipMemcpyDtoD.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    dev = trlm.Device()
+    sweep = Sweep(trlm, dev)
+    src, dst = dev.empty(PROBE_COPY_BYTES), dev.empty(PROBE_COPY_BYTES)
+    dev.sync()
+    for _ in range(3):
+        assert rt.hipMemcpyDtoD(dst, src, PROBE_COPY_BYTES) == 0
+    head = [it for it in sweep.items if it[0] == "lm_head_fwd"][0]
+    for _ in range(3):
+        sweep.run(head)
+    dev.sync()
+    print("probe: 3 copies of %d bytes, 3 x %s" % (PROBE_COPY_BYTES, "%s/split%d" % dev.last_variant()), flush=True)
+    dev.free(src)
+    dev.free(dst)
+    sweep.close()
+    dev.close()
+
+
+def traffic_summarize(fetch_dir, write_dir):
+    """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the probe's copies and
+    LM-head GEMMs; each counter is scaled by the factor that makes it read
+    the copy's true size, and the LM head's scaled sum is its HBM traffic."""
+    import csv
+    import glob
+
+    def per_kernel(d, counter):
+        vals = {}
+        for f in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            for r in csv.DictReader(open(f)):
+                if r["Counter_Name"] != counter:
+                    continue
+                k = "copy" if "copyBuffer" in r["Kernel_Name"] else (
+                    "head" if r["Kernel_Name"].startswith("k_gemm_nt") else None)
+                if k:
+                    vals.setdefault(k, {}).setdefault(r["Dispatch_Id"], 0.0)
+                    vals[k][r["Dispatch_Id"]] += float(r["Counter_Value"])
+        return {k: sorted(v.values()) for k, v in vals.items()}
+
+    fe, wr = per_kernel(fetch_dir, "FETCH_SIZE"), per_kernel(write_dir, "WRITE_SIZE")
+    kib = PROBE_COPY_BYTES / 1024.0
+    f_fetch = kib / np.median(fe["copy"])
+    f_write = kib / np.median(wr["copy"])
+    head_f = np.median(fe["head"]) * f_fetch * 1024.0
+    head_w = np.median(wr["head"]) * f_write * 1024.0
+    M_, N_, K_ = M, V, D
+    alg = 4.0 * (M_ * K_ + N_ * K_ + M_ * N_)
+    print("copy calibration: FETCH_SIZE %.0f KiB -> factor %.4f; WRITE_SIZE %.0f KiB -> factor %.4f (copy of %d B)"
+          % (np.median(fe["copy"]), f_fetch, np.median(wr["copy"]), f_write, PROBE_COPY_BYTES))
+    print("lm_head_fwd per launch: FETCH %.1f MB, WRITE %.1f MB (scaled)" % (head_f / 1e6, head_w / 1e6))
+    print("algorithmic bytes (A + B read once, C written once): %.1f MB" % (alg / 1e6))
+    print("traffic_bytes %d" % int(head_f + head_w))
+
+
+def traffic_bytes():
+    """The LM-head forward's measured HBM bytes per launch, from the committed
+    counter summary (null when it was not measured)."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes "):
+                return int(line.split()[1])
+    except OSError:
+        pass
+    return None
+
+
 def main():
+    if len(sys.argv) > 3 and sys.argv[1] == "--traffic-summarize":
+        traffic_summarize(sys.argv[2], sys.argv[3])
+        return
     if len(sys.argv) > 2 and sys.argv[1] == "--summarize":
         summarize_profile(sys.argv[2])
         return
@@ -318,6 +396,8 @@ def main():
                     help="time every GEMM tile variant / split-K factor on the sweep shapes and exit")
     ap.add_argument("--tune-out", default=None, help="with --tune: write every timing as JSON lines here")
     ap.add_argument("--decode-only", action="store_true", help="only the config-5 decode measurement (JSON line)")
+    ap.add_argument("--traffic-probe", action="store_true",
+                    help="only the dispatches the FETCH_SIZE / WRITE_SIZE counter passes read")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
@@ -331,6 +411,9 @@ def main():
         return
     if args.decode_only:
         print(json.dumps(decode_benchmark(trlm)), flush=True)
+        return
+    if args.traffic_probe:
+        traffic_probe(trlm)
         return
     if args.model_only:
         print(json.dumps(model_benchmarks(trlm, args.steps, args.warmup)), flush=True)
@@ -368,7 +451,7 @@ def main():
         "pct_fp32_mfma_peak": round(100.0 * value / PEAK_FP32_MFMA, 2),
         "gemm_tflops": per_gemm, "gemm_variant": variants,
         "roofline": {"bound": "mfma", "achieved": round(achieved, 3), "peak": PEAK_FP32_MFMA, "unit": "TFLOP/s",
-                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": None,
+                     "frac": round(achieved / PEAK_FP32_MFMA, 4), "traffic": traffic_bytes(),
                      "kernel": "%s (LM head fwd 8192x31769x384 NT)" % variants["lm_head_fwd"],
                      "launch_ms": round(head_ms, 4)},
     }

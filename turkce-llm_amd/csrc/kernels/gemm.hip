@@ -16,6 +16,13 @@
 //  - Operands are staged through double-buffered LDS, one barrier per
 //    BK=16 (or 32) step; the next global tile is prefetched into registers while the
 //    current one feeds the matrix cores.
+//  - Interior tiles run a software-pipelined loop: the operand fragments of
+//    the next 8-k chunk are read from LDS while the current chunk's MFMAs
+//    run, the next tile is written to LDS before the last chunk, and that
+//    chunk's MFMAs are issued after the barrier, where they cover the reads
+//    of the next tile's first chunk.  A wave raises its priority while it
+//    issues MFMAs, so the waves sharing a SIMD fall out of step and one
+//    wave's LDS/barrier phase overlaps another's matrix work.
 //  - A K-contiguous operand is kept K-contiguous in LDS and read with one
 //    128-bit LDS read per 4 MFMA steps: lane l feeds k = kk+4*(l/32)+s at
 //    step s, a permutation of k that both operands share.  An MN-contiguous
@@ -165,7 +172,8 @@ struct TileStream {
     }
 };
 
-template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED, bool FULL>
+// Edge tiles and the scalar-load variants: every load checked.
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
 __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* A, const float* B, int m0, int n0,
                                               int kb, int ke, float* lds, f32x16 (&acc)[BM / 64][BN / 64]) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
@@ -178,20 +186,9 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* 
     const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
 
     f32x4 ra[NLA > 0 ? NLA : 1], rb[NLB > 0 ? NLB : 1];
-    TileStream<BM, BK, AK> sa;
-    TileStream<BN, BK, BK_> sb;
-    if (FULL) {
-        sa.init(A, p.lda, m0, kb);
-        sb.init(B, p.ldb, n0, kb);
-    }
     auto gload = [&](int k0) {
-        if (FULL) {
-            sa.load(ra);
-            sb.load(rb);
-        } else {
-            load_tile<BM, BK, AK, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
-            load_tile<BN, BK, BK_, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
-        }
+        load_tile<BM, BK, AK, ALIGNED>(A, p.lda, m0, p.M, k0, ke, ra);
+        load_tile<BN, BK, BK_, ALIGNED>(B, p.ldb, n0, p.N, k0, ke, rb);
     };
     auto lstore = [&](int buf) {
         store_tile<BM, BK, AK>(lds + buf * (ASZ + BSZ), ra);
@@ -222,10 +219,91 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* 
                 for (int i = 0; i < FM; i++)
 #pragma unroll
                     for (int j = 0; j < FN; j++)
-                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[i][s], fb[j][s], acc[i][j], 0, 0, 0);
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[j][s], fa[i][s], acc[i][j], 0, 0, 0);
         }
         if (kt + 1 < nk) lstore(cur ^ 1);
         __syncthreads();
+    }
+}
+
+template <int R, int BK, bool KMAJOR, int NF>
+__device__ __forceinline__ void fetch_frags(const float* lds, int rb0, int kk, int lane, f32x4 (&f)[NF]) {
+#pragma unroll
+    for (int i = 0; i < NF; i++) f[i] = fetch_frag<R, BK, KMAJOR>(lds, rb0 + i * 32, kk, lane);
+}
+
+// Interior tiles (every load in bounds, k-range a whole number of BK steps):
+// fragments double-buffered per 8-k chunk, next tile stored before the last
+// chunk, last chunk's MFMAs after the barrier.
+template <int TA, int TB, int BM, int BN, int BK>
+__device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const float* A, const float* B, int m0,
+                                                   int n0, int kb, int ke, float* lds,
+                                                   f32x16 (&acc)[BM / 64][BN / 64]) {
+    constexpr bool AK = (TA == 0);   // A K-contiguous
+    constexpr bool BK_ = (TB == 1);  // B K-contiguous
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
+    constexpr int NLA = BM * BK / 4 / 256, NLB = BN * BK / 4 / 256;
+    constexpr int NC = BK / 8;
+    static_assert(NC % 2 == 0, "fragment buffers alternate per 8-k chunk");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+    f32x4 ra[NLA], rb[NLB];
+    TileStream<BM, BK, AK> sa;
+    TileStream<BN, BK, BK_> sb;
+    sa.init(A, p.lda, m0, kb);
+    sb.init(B, p.ldb, n0, kb);
+    const int nk = (ke - kb) / BK;
+    sa.load(ra);
+    sb.load(rb);
+    store_tile<BM, BK, AK>(lds, ra);
+    store_tile<BN, BK, BK_>(lds + ASZ, rb);
+    if (nk > 1) {
+        sa.load(ra);
+        sb.load(rb);
+    }
+    __syncthreads();
+    f32x4 fa[2][FM], fb[2][FN];
+    fetch_frags<BM, BK, AK, FM>(lds, wm0, 0, lane, fa[0]);
+    fetch_frags<BN, BK, BK_, FN>(lds + ASZ, wn0, 0, lane, fb[0]);
+    for (int kt = 0; kt < nk; kt++) {
+        const float* la = lds + (kt & 1) * (ASZ + BSZ);
+        float* ln = lds + ((kt & 1) ^ 1) * (ASZ + BSZ);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int u = c & 1, v = u ^ 1;
+            if (c + 1 < NC) {
+                fetch_frags<BM, BK, AK, FM>(la, wm0, (c + 1) * 8, lane, fa[v]);
+                fetch_frags<BN, BK, BK_, FN>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
+            } else {
+                // Last chunk of this tile: its fragments are in registers, so
+                // the other buffer can take the next tile before the barrier.
+                if (kt + 1 < nk) {
+                    store_tile<BM, BK, AK>(ln, ra);
+                    store_tile<BN, BK, BK_>(ln + ASZ, rb);
+                }
+                __syncthreads();
+                if (kt + 1 < nk) {
+                    fetch_frags<BM, BK, AK, FM>(ln, wm0, 0, lane, fa[v]);
+                    fetch_frags<BN, BK, BK_, FN>(ln + ASZ, wn0, 0, lane, fb[v]);
+                    if (kt + 2 < nk) {
+                        sa.load(ra);
+                        sb.load(rb);
+                    }
+                }
+            }
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u][j][s], fa[u][i][s], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+        }
     }
 }
 
@@ -261,47 +339,93 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    // Interior tiles whose k-range is whole BK steps take the check-free
-    // loop; edge tiles (and the scalar-load variants) the guarded one.
+    // Interior tiles whose k-range is whole BK steps take the pipelined,
+    // check-free loop; edge tiles (and the scalar-load variants) the guarded one.
     const bool full = ALIGNED && m0 + BM <= p.M && n0 + BN <= p.N && ke > kb && (ke - kb) % BK == 0;
-    if (full) gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, ALIGNED>(p, A, B, m0, n0, kb, ke, lds, acc);
-    else gemm_mainloop<TA, TB, BM, BN, BK, ALIGNED, false>(p, A, B, m0, n0, kb, ke, lds, acc);
+    if constexpr (ALIGNED) {
+        if (full) gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc);
+        else gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kb, ke, lds, acc);
+    } else {
+        gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc);
+    }
 
-    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.  C and
-    // resid values are loaded four rows at a time before the four stores:
-    // the compiler cannot prove that C aliases neither, so a load after a
-    // store would otherwise wait for the one before it.
-    const int half = lane >> 5, col_l = lane & 31;
+    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.
+    // The MFMAs take the B fragment as their first operand, so each 32x32
+    // accumulator block holds C^T: lane l owns row m = l%32 of the block and,
+    // in registers 4g..4g+3, its four consecutive columns 8g + 4*(l/32) + q --
+    // one 16-byte run of a row of C, stored (and C, resid, bias read) as one
+    // f32x4 where alignment allows.  A block's loads all precede its stores:
+    // the compiler cannot prove that C aliases neither resid nor bias, so a
+    // load after a store would otherwise wait for it.
+    const int half = lane >> 5, ml = lane & 31;
+    const bool vec = ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(p.resid) |
+                       reinterpret_cast<uintptr_t>(p.bias)) & 15) == 0 &&
+                     ((p.ldc | (p.resid ? p.ldr : 0)) & 3) == 0;
+    const bool nfull = n0 + BN <= p.N;
+    constexpr int EPI_GROUPS = 2;   // 16-byte runs loaded ahead of their stores
 #pragma unroll
-    for (int i = 0; i < FM; i++)
+    for (int i = 0; i < FM; i++) {
+        const int row = m0 + wm0 + i * 32 + ml;
+        if (row >= p.M) continue;
+        float* crow = C + (long long)row * p.ldc;
+        const float* rrow = p.resid + (long long)row * p.ldr;
 #pragma unroll
         for (int j = 0; j < FN; j++) {
-            const int col = n0 + wn0 + j * 32 + col_l;
-            if (col >= p.N) continue;
-            const float bv = p.bias ? p.bias[col] : 0.f;
+            const int nb = n0 + wn0 + j * 32 + 4 * half;
+            if (vec && nfull) {
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                float cv[4], rv[4];
+                for (int g0 = 0; g0 < 4; g0 += EPI_GROUPS) {
+                    f32x4 cv[EPI_GROUPS], rv[EPI_GROUPS], bv[EPI_GROUPS];
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int row = m0 + wm0 + i * 32 + 8 * g + 4 * half + q;
-                    const bool ok = row < p.M;
-                    cv[q] = (ok && p.beta != 0.f) ? C[(long long)row * p.ldc + col] : 0.f;
-                    rv[q] = (ok && p.resid) ? p.resid[(long long)row * p.ldr + col] : 0.f;
+                    for (int e = 0; e < EPI_GROUPS; e++) {
+                        const int n = nb + 8 * (g0 + e);
+                        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                        cv[e] = p.beta != 0.f ? *(const f32x4*)(crow + n) : z;
+                        rv[e] = p.resid ? *(const f32x4*)(rrow + n) : z;
+                        bv[e] = p.bias ? *(const f32x4*)(p.bias + n) : z;
+                    }
+#pragma unroll
+                    for (int e = 0; e < EPI_GROUPS; e++) {
+                        const int g = g0 + e;
+                        f32x4 v;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            float x = p.alpha * acc[i][j][4 * g + q];
+                            if (p.beta != 0.f) x = x + p.beta * cv[e][q];
+                            if (p.bias) x = x + bv[e][q];
+                            if (p.resid) x = rv[e][q] + x;
+                            v[q] = x;
+                        }
+                        *(f32x4*)(crow + nb + 8 * g) = v;
+                    }
                 }
+            } else {
 #pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int row = m0 + wm0 + i * 32 + 8 * g + 4 * half + q;
-                    if (row < p.M) {
-                        float v = p.alpha * acc[i][j][4 * g + q];
-                        if (p.beta != 0.f) v = v + p.beta * cv[q];
-                        if (p.bias) v = v + bv;
-                        if (p.resid) v = rv[q] + v;
-                        C[(long long)row * p.ldc + col] = v;
+                for (int g = 0; g < 4; g++) {
+                    float cv[4], rv[4], bv[4];
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int n = nb + 8 * g + q;
+                        const bool ok = n < p.N;
+                        cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
+                        rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
+                        bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
+                    }
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        const int n = nb + 8 * g + q;
+                        if (n < p.N) {
+                            float x = p.alpha * acc[i][j][4 * g + q];
+                            if (p.beta != 0.f) x = x + p.beta * cv[q];
+                            if (p.bias) x = x + bv[q];
+                            if (p.resid) x = rv[q] + x;
+                            crow[n] = x;
+                        }
                     }
                 }
             }
         }
+    }
 }
 
 #define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE)                                 \

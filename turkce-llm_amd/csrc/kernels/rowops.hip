@@ -392,17 +392,20 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     float* z = logits + row * ld;
     const bool vec = ((ld & 3) == 0);
     float m = -INFINITY, s = 0.f;
+    const float L2E = 1.4426950408889634f;
     if (vec) {
+        // per float4: one rescale to the new running max, then four
+        // exponentials (exp2 of log2e-scaled differences, one instruction)
         const int nq = (V + 3) >> 2;
         for (int q = threadIdx.x; q < nq; q += 256) {
             f32x4 v = ((const f32x4*)z)[q];
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                if (4 * q + e >= V) break;
-                float x = v[e];
-                if (x > m) { s = s * expf(m - x) + 1.f; m = x; }
-                else s += expf(x - m);
-            }
+            for (int e = 0; e < 4; e++)
+                if (4 * q + e >= V) v[e] = -INFINITY;
+            const float nm = fmaxf(fmaxf(m, fmaxf(v[0], v[1])), fmaxf(v[2], v[3]));
+            s = s * exp2f((m - nm) * L2E) + ((exp2f((v[0] - nm) * L2E) + exp2f((v[1] - nm) * L2E)) +
+                                             (exp2f((v[2] - nm) * L2E) + exp2f((v[3] - nm) * L2E)));
+            m = nm;
         }
     } else {
         for (int j = threadIdx.x; j < V; j += 256) {
@@ -438,7 +441,7 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
 #pragma unroll
             for (int e = 0; e < 4; e++) {
                 int j = 4 * q + e;
-                float p = (j < V) ? expf(v[e] - M) * inv : 0.f;
+                float p = (j < V) ? exp2f((v[e] - M) * L2E) * inv : 0.f;
                 if (j == (int)t) p -= 1.0f;
                 v[e] = p * grad_scale;
             }
