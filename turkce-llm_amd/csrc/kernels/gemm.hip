@@ -307,6 +307,101 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
     }
 }
 
+// Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v, for one
+// wave's (BM/2)x(BN/2) block at rows r0.., columns c0...
+// The MFMAs take the B fragment as their first operand, so each 32x32
+// accumulator block holds C^T: lane l owns row m = l%32 of the block and, in
+// registers 4g..4g+3, its four consecutive columns 8g + 4*(l/32) + q -- one
+// 16-byte run of a row of C.  Where the operands are 16-byte aligned and the
+// tile's columns are all in range, each run is read and stored as one f32x4,
+// and the loads of two column blocks are issued together ahead of their
+// stores (the compiler cannot move a load above a store that may alias it,
+// so interleaving them would expose every load's latency).  Everything else
+// takes the per-element path.
+template <int BM, int BN>
+__device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, const f32x16 (&acc)[BM / 64][BN / 64],
+                                              int r0, int c0, int lane) {
+    constexpr int FM = BM / 64, FN = BN / 64;
+    constexpr int JG = FN < 2 ? FN : 2;
+    const int half = lane >> 5, ml = lane & 31;
+    const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
+    const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;
+    const bool vec = !(p.beta != 0.f && p.resid) &&
+                     ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(p.resid) |
+                       reinterpret_cast<uintptr_t>(p.bias)) & 15) == 0 &&
+                     ((p.ldc | (p.resid ? p.ldr : 0)) & 3) == 0 && c0 + BN / 2 <= p.N;
+    if (vec) {
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            const int row = r0 + i * 32 + ml;
+            if (row >= p.M) continue;
+            float* crow = C + (long long)row * p.ldc;
+            const float* arow = addp + (long long)row * ldadd;
+#pragma unroll
+            for (int j0 = 0; j0 < FN; j0 += JG) {
+                f32x4 av[JG][4], bv[JG][4];
+#pragma unroll
+                for (int jj = 0; jj < JG; jj++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
+                        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                        av[jj][g] = addp ? *(const f32x4*)(arow + n) : z;
+                        bv[jj][g] = p.bias ? *(const f32x4*)(p.bias + n) : z;
+                    }
+#pragma unroll
+                for (int jj = 0; jj < JG; jj++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++) {
+                        f32x4 v;
+#pragma unroll
+                        for (int q = 0; q < 4; q++) {
+                            float x = p.alpha * acc[i][j0 + jj][4 * g + q];
+                            if (p.beta != 0.f) x = x + p.beta * av[jj][g][q];
+                            if (p.bias) x = x + bv[jj][g][q];
+                            if (p.resid) x = av[jj][g][q] + x;
+                            v[q] = x;
+                        }
+                        *(f32x4*)(crow + c0 + (j0 + jj) * 32 + 8 * g + 4 * half) = v;
+                    }
+            }
+        }
+        return;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        const int row = r0 + i * 32 + ml;
+        if (row >= p.M) continue;
+        float* crow = C + (long long)row * p.ldc;
+        const float* rrow = p.resid + (long long)row * p.ldr;
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                float cv[4], rv[4], bv[4];
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n = c0 + j * 32 + 8 * g + 4 * half + q;
+                    const bool ok = n < p.N;
+                    cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
+                    rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
+                    bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
+                }
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    const int n = c0 + j * 32 + 8 * g + 4 * half + q;
+                    if (n < p.N) {
+                        float x = p.alpha * acc[i][j][4 * g + q];
+                        if (p.beta != 0.f) x = x + p.beta * cv[q];
+                        if (p.bias) x = x + bv[q];
+                        if (p.resid) x = rv[q] + x;
+                        crow[n] = x;
+                    }
+                }
+            }
+    }
+}
+
 template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
 __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
@@ -349,83 +444,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
         gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc);
     }
 
-    // Epilogue: v = alpha*acc (+ beta*C) (+ bias[n]); C = resid + v.
-    // The MFMAs take the B fragment as their first operand, so each 32x32
-    // accumulator block holds C^T: lane l owns row m = l%32 of the block and,
-    // in registers 4g..4g+3, its four consecutive columns 8g + 4*(l/32) + q --
-    // one 16-byte run of a row of C, stored (and C, resid, bias read) as one
-    // f32x4 where alignment allows.  A block's loads all precede its stores:
-    // the compiler cannot prove that C aliases neither resid nor bias, so a
-    // load after a store would otherwise wait for it.
-    const int half = lane >> 5, ml = lane & 31;
-    const bool vec = ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(p.resid) |
-                       reinterpret_cast<uintptr_t>(p.bias)) & 15) == 0 &&
-                     ((p.ldc | (p.resid ? p.ldr : 0)) & 3) == 0;
-    const bool nfull = n0 + BN <= p.N;
-    constexpr int EPI_GROUPS = 2;   // 16-byte runs loaded ahead of their stores
-#pragma unroll
-    for (int i = 0; i < FM; i++) {
-        const int row = m0 + wm0 + i * 32 + ml;
-        if (row >= p.M) continue;
-        float* crow = C + (long long)row * p.ldc;
-        const float* rrow = p.resid + (long long)row * p.ldr;
-#pragma unroll
-        for (int j = 0; j < FN; j++) {
-            const int nb = n0 + wn0 + j * 32 + 4 * half;
-            if (vec && nfull) {
-#pragma unroll
-                for (int g0 = 0; g0 < 4; g0 += EPI_GROUPS) {
-                    f32x4 cv[EPI_GROUPS], rv[EPI_GROUPS], bv[EPI_GROUPS];
-#pragma unroll
-                    for (int e = 0; e < EPI_GROUPS; e++) {
-                        const int n = nb + 8 * (g0 + e);
-                        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                        cv[e] = p.beta != 0.f ? *(const f32x4*)(crow + n) : z;
-                        rv[e] = p.resid ? *(const f32x4*)(rrow + n) : z;
-                        bv[e] = p.bias ? *(const f32x4*)(p.bias + n) : z;
-                    }
-#pragma unroll
-                    for (int e = 0; e < EPI_GROUPS; e++) {
-                        const int g = g0 + e;
-                        f32x4 v;
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            float x = p.alpha * acc[i][j][4 * g + q];
-                            if (p.beta != 0.f) x = x + p.beta * cv[e][q];
-                            if (p.bias) x = x + bv[e][q];
-                            if (p.resid) x = rv[e][q] + x;
-                            v[q] = x;
-                        }
-                        *(f32x4*)(crow + nb + 8 * g) = v;
-                    }
-                }
-            } else {
-#pragma unroll
-                for (int g = 0; g < 4; g++) {
-                    float cv[4], rv[4], bv[4];
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int n = nb + 8 * g + q;
-                        const bool ok = n < p.N;
-                        cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
-                        rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
-                        bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
-                    }
-#pragma unroll
-                    for (int q = 0; q < 4; q++) {
-                        const int n = nb + 8 * g + q;
-                        if (n < p.N) {
-                            float x = p.alpha * acc[i][j][4 * g + q];
-                            if (p.beta != 0.f) x = x + p.beta * cv[q];
-                            if (p.bias) x = x + bv[q];
-                            if (p.resid) x = rv[q] + x;
-                            crow[n] = x;
-                        }
-                    }
-                }
-            }
-        }
-    }
+    gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
 }
 
 #define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE)                                 \
@@ -442,16 +461,17 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
 // name: k_gemm_<layout>_<BM>x<BN>[_k32][_u]
 //   _k32: 32-deep k step (one barrier per 32 k instead of 16)
 //   _u:   unaligned operands (scalar loads), 16-deep k step
-// Waves own (BM/2)x(BN/2): 256x128 / 128x256 tiles hold 8 accumulator blocks
-// per wave and are held to 2 waves per SIMD (<= 128 VGPRs + 128 AGPRs).
+// Waves own (BM/2)x(BN/2).  The last argument is the register budget as
+// resident waves per SIMD: the largest count the variant's LDS allows (2 for
+// the 8-accumulator-block 256x128 / 128x256 tiles), short of spilling.
 GEMM_LAYOUTS(256x128, 256, 128, 16, 2)
 GEMM_LAYOUTS(128x256, 128, 256, 16, 2)
-GEMM_LAYOUTS(128x128, 128, 128, 16, 1)
-GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 1)
-GEMM_LAYOUTS(64x128, 64, 128, 16, 1)
-GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 1)
-GEMM_LAYOUTS(64x64, 64, 64, 16, 1)
-GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 1)
+GEMM_LAYOUTS(128x128, 128, 128, 16, 3)
+GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 2)
+GEMM_LAYOUTS(64x128, 64, 128, 16, 4)
+GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 2)
+GEMM_LAYOUTS(64x64, 64, 64, 16, 8)
+GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 4)
 GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1)
 GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1)
 GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, 16, false, 1)
