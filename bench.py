@@ -389,6 +389,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-model", action="store_true", help="skip the forward/training measurements")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--no-decode", action="store_true",
+                    help="skip the config-5 decode leg (its replayed HIP graph does not run under "
+                         "rocprofv3's kernel trace, which ends the process with SIGSEGV)")
     ap.add_argument("--model-only", action="store_true",
                     help="only the B8 T1024 forward/train measurements (for focused profiling); "
                          "prints them as a JSON line without the sweep")
@@ -459,7 +462,7 @@ def main():
         log("model: forward / train at B=%d T=%d" % (B, T))
         line.update({k: (round(v, 3) if isinstance(v, float) else v)
                      for k, v in model_benchmarks(trlm, max(3, args.steps // 2), args.warmup).items()})
-    if not args.no_model:
+    if not args.no_model and not args.no_decode:
         log("decode: config 5")
         line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode_benchmark(trlm).items()})
     if not args.no_cpu:
