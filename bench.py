@@ -157,10 +157,44 @@ def model_benchmarks(trlm, steps, warmup):
         out = {"fwd_ms": fwd * 1e3, "fwd_tokens_per_s": M / fwd, "train_ms": trn * 1e3,
                "train_tokens_per_s": M / trn, "train_loss_last": float(loss),
                "fwd_tflops_algorithmic": 625.16e9 / fwd / 1e12, "train_tflops_algorithmic": 1875.5e9 / trn / 1e12}
+        out.update(driver_benchmarks(trlm, tr, adam, rng, steps, warmup))
     finally:
         tr.destroy()
         hm.close()
     return out
+
+
+def driver_benchmarks(trlm, tr, adam, rng, steps, warmup):
+    """The reference driver's full step (train_lm_gpu.c:212-223: schedule,
+    sampled batch, forward/backward, grad norm, clip, AdamW) at B8 T1024 on
+    a synthetic 4M-token stream: as the reference's call sequence (host
+    waits inside every call) and queued (gpu_trainer_train_steps)."""
+    _, hip = trlm.libs()
+    tokens = rng.integers(0, V, 1 << 22, dtype=np.uint32)
+    s = trlm.TrlmSchedule()
+    s.warmup_steps, s.total_steps, s.peak_lr, s.min_lr = 100, 10000, 6e-4, 6e-5
+    s.grad_clip, s.weight_decay, s.seed_base = 1.0, 0.1, 2026
+    ids = np.zeros(M, np.uint32)
+    tgt = np.zeros(M, np.uint32)
+
+    def sequence(first, n):
+        for step in range(first, first + n):
+            adam.opt.lr = hip.trlm_lr_warmup_cosine(step, s.warmup_steps, s.total_steps, s.peak_lr, s.min_lr)
+            hip.gpu_trainer_sample_batch(tokens, tokens.size, T, B, s.seed_base + step, ids, tgt)
+            tr.forward_backward(ids, tgt)
+            norm = tr.grad_norm()
+            tr.adamw_step(adam, s.weight_decay, (s.grad_clip / norm) if norm > s.grad_clip else 1.0)
+
+    sequence(0, warmup)
+    t0 = time.perf_counter()
+    sequence(warmup, steps)
+    seq = (time.perf_counter() - t0) / steps
+    tr.train_steps(adam, tokens, s, 0, warmup)
+    t0 = time.perf_counter()
+    losses, _, _ = tr.train_steps(adam, tokens, s, warmup, steps)
+    queued = (time.perf_counter() - t0) / steps
+    return {"driver_step_ms": queued * 1e3, "driver_tokens_per_s": M / queued,
+            "driver_step_ms_call_sequence": seq * 1e3, "driver_loss_last": float(losses[-1])}
 
 
 DEC_B, DEC_PROMPT, DEC_CTX = 64, 128, 1024

@@ -9,7 +9,10 @@
  *   - AdamW (decoupled weight decay; the reference's Adam has none,
  *     training/adam.c:43-52);
  *   - a raw fp32 GEMM on device buffers and stream-event timing, for the
- *     model-shape GEMM sweep and its tests.
+ *     model-shape GEMM sweep and its tests;
+ *   - TRLM v1 checkpoints straight from / to the device, a KV-cache decoder,
+ *     and the training driver's loop (lr schedule, clipping, validation
+ *     windows) queued on the device.
  */
 #ifndef TRLM_EXT_H
 #define TRLM_EXT_H
@@ -97,6 +100,37 @@ void gpu_decoder_sample(TrlmDecoder* d, PCGState* rngs, f32 temperature, u32* ou
 /* prefill + greedy generation of `steps` tokens per sequence; out
  * [batch][steps] (prompt_len + steps <= max_ctx) */
 void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, u32* out);
+
+/* ---- training driver loop (training/train_lm_gpu.c:212-223, 241-258) ----
+ * The reference's driver, per step: lr = lr_warmup_cosine(step, ...);
+ * batch = gpu_trainer_sample_batch(..., seed_base + step); loss =
+ * forward_backward; norm = grad_norm; scale = clip/norm when norm > clip,
+ * else 1; adam_step_scaled(scale).  gpu_trainer_train_steps runs steps
+ * first_step .. first_step+n_steps-1 of that loop with the same results bit
+ * for bit, but queued: the batches are prepared on the host while the device
+ * runs, and the loss mean, grad norm and clip scale stay on the device until
+ * the call returns (one wait per call instead of several per step).
+ * losses / grad_norms / lrs (each n_steps long, any may be NULL) receive each
+ * step's loss, norm and learning rate; opt->lr holds the last step's rate. */
+typedef struct TrlmSchedule {
+    u64 warmup_steps, total_steps;   /* lr_warmup_cosine(step, warmup, total, peak, min) */
+    f32 peak_lr, min_lr;
+    f64 grad_clip;                   /* clip when the norm exceeds this; <= 0: never */
+    f32 weight_decay;                /* 0: the reference's Adam; > 0: AdamW (decoupled) */
+    u64 seed_base;                   /* step s samples with seed_base + s (reference: 2026) */
+} TrlmSchedule;
+void gpu_trainer_train_steps(GpuTrainer* g, AdamOptimizer* opt, const u32* tokens, u64 num_tokens,
+                             const TrlmSchedule* s, u64 first_step, u32 n_steps, f32* losses, f64* grad_norms,
+                             f32* lrs);
+/* The driver's validation loss: val_batches x batch fixed windows spread
+ * evenly over tokens[train_tokens .. train_tokens+val_tokens) (stride
+ * (val_tokens - T - 1) / (val_batches * batch)), the f32 sum of the
+ * batches' eval losses in order, divided by val_batches.  tokens holds at
+ * least train_tokens + val_tokens ids. */
+f32 gpu_trainer_eval_windows(GpuTrainer* g, const u32* tokens, u64 train_tokens, u64 val_tokens, u32 val_batches);
+/* lr_warmup_cosine (training/lr_schedule.c:6-15): linear warmup to peak over
+ * warmup steps, then half a cosine from peak to min by total_steps. */
+f32 trlm_lr_warmup_cosine(u64 step, u64 warmup_steps, u64 total_steps, f32 peak_lr, f32 min_lr);
 
 /* Stream-event timing on the current context's stream. */
 typedef struct TrlmTimer { hipEvent_t start, stop; } TrlmTimer;

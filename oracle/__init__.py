@@ -72,6 +72,7 @@ def _load():
                                 C.c_float, C.c_float, C.c_float, C.c_float, C.c_float]),
         "or_argmax": (C.c_uint32, [f32p, C.c_uint32]),
         "or_sample_next": (C.c_uint32, [f32p, C.c_uint32, C.c_float, C.POINTER(Pcg), f32p]),
+        "or_lr_warmup_cosine": (C.c_float, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_float]),
     }
     for name, (res, args) in sig.items():
         fn = getattr(lib, name)
@@ -250,6 +251,11 @@ def trlm_parse(data, shapes, want_opt):
     return params, np.concatenate(m), np.concatenate(v), t
 
 
+def lr_warmup_cosine(step, warmup, total, peak, min_lr):
+    """The reference's learning-rate schedule (training/lr_schedule.c) as f32."""
+    return np.float32(lib().or_lr_warmup_cosine(step, warmup, total, peak, min_lr))
+
+
 def sample_next(row, temperature, pcg):
     """sample_next on one row of logits; pcg (a Pcg) advances by one draw."""
     row = np.ascontiguousarray(row, np.float32)
@@ -308,6 +314,7 @@ class Reference:
         h.refh_adam_step.argtypes = [cfgp, f32p, f32p, f32p, f32p, C.c_uint64, C.c_float,
                                      C.c_float, C.c_float, C.c_float]
         h.refh_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
+        h.refh_lr_schedule.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64, C.c_float, C.c_float, f32p]
         h.refh_time_train_step.restype = C.c_double
         h.refh_time_train_step.argtypes = [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32,
                                            C.c_uint64, f32p, f32p, C.c_int]
@@ -368,6 +375,11 @@ class Reference:
         ok = self.h.refh_checkpoint_load(C.byref(c), path.encode(), p, m.ctypes.data if want_opt else None,
                                          v.ctypes.data if want_opt else None, C.byref(t), int(want_opt))
         return (p, m, v, t.value) if ok else None
+
+    def lr_schedule(self, first, n, warmup, total, peak, min_lr):
+        out = np.zeros(n, np.float32)
+        self.h.refh_lr_schedule(first, n, warmup, total, peak, min_lr, out)
+        return out
 
     def matmul(self, A, B):
         A = np.ascontiguousarray(A, np.float32)

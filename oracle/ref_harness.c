@@ -57,6 +57,7 @@ static struct {
     f32 (*m_sinf)(f32); f32 (*m_cosf)(f32);
     bool32 (*checkpoint_save)(const char*, Node**, u32, const AdamOptimizer*);
     bool32 (*checkpoint_load)(Allocator*, const char*, Node**, u32, AdamOptimizer*);
+    f32 (*lr_warmup_cosine)(u64, u64, u64, f32, f32);
     int ok;
 } R;
 
@@ -74,6 +75,7 @@ int refh_open(const char* lib_path) {
     LOAD(m_sqrt); LOAD(m_exp); LOAD(m_log); LOAD(m_pow); LOAD(m_sin); LOAD(m_cos);
     LOAD(m_powf); LOAD(m_expf); LOAD(m_logf); LOAD(m_sqrtf); LOAD(m_sinf); LOAD(m_cosf);
     LOAD(checkpoint_save); LOAD(checkpoint_load);
+    LOAD(lr_warmup_cosine);
     R.ok = 1;
     return 0;
 }
@@ -95,6 +97,11 @@ double refh_m(int which, double x, double y) {
         case 15: return (double)R.m_cosf((f32)x);
         default: return 0.0;
     }
+}
+
+/* lr_warmup_cosine (training/lr_schedule.c) for steps first..first+n-1. */
+void refh_lr_schedule(u64 first, u32 n, u64 warmup, u64 total, f32 peak, f32 min_lr, f32* out) {
+    for (u32 i = 0; i < n; i++) out[i] = R.lr_warmup_cosine(first + i, warmup, total, peak, min_lr);
 }
 
 void refh_pcg_u32(u64 sa, u64 sb, u32 n, u32* out) {

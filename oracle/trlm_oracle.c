@@ -183,6 +183,17 @@ float or_m_powf(float b, float e) { return (float)or_m_pow((double)b, (double)e)
 float or_m_sinf(float x) { return (float)or_m_sin((double)x); }
 float or_m_cosf(float x) { return (float)or_m_cos((double)x); }
 
+/* training/lr_schedule.c:6-15: warmup (step+1)/W of peak, then
+ * min + (peak-min) * (1 + cos(pi*p))/2 in f64 with p clamped to 1. */
+float or_lr_warmup_cosine(uint64_t step, uint64_t warmup, uint64_t total, float peak, float min_lr) {
+    if (warmup > 0 && step < warmup) return peak * (float)(step + 1) / (float)warmup;
+    if (total <= warmup) return min_lr;
+    double p = (double)(step - warmup) / (double)(total - warmup);
+    if (p > 1.0) p = 1.0;
+    double c = 0.5 * (1.0 + or_m_cos(3.14159265358979323846 * p));
+    return (float)((double)min_lr + ((double)peak - (double)min_lr) * c);
+}
+
 /* ======================= PCG32 (runtime/prng.c) ======================= */
 
 uint32_t or_pcg_next_u32(OrPcg* r) {     /* prng.c:10-17, pcg_setseq_64_xsh_rr_32 */

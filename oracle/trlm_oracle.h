@@ -49,6 +49,8 @@ double or_m_log(double x);
 double or_m_pow(double b, double e);
 double or_m_sin(double x);
 double or_m_cos(double x);
+/* lr_warmup_cosine (training/lr_schedule.c:6-15) */
+float or_lr_warmup_cosine(uint64_t step, uint64_t warmup, uint64_t total, float peak, float min_lr);
 float or_m_sqrtf(float x);
 float or_m_expf(float x);
 float or_m_logf(float x);

@@ -3,7 +3,8 @@
 Outputs (next to this file, git-ignored, shipped to the GPU box as built):
   trlm_kernels.hsaco  gfx950 code object with every kernel (hipcc --genco)
   libtrlm_hip.so      the drop-in C library: hip_backend.c, trlm_gemm.c,
-                      gpu_train.c, gpu_decode.c, checkpoint.c, gpu_ops.c (gcc, HIP runtime API)
+                      gpu_train.c, gpu_decode.c, checkpoint.c, train_loop.c,
+                      gpu_ops.c (gcc, HIP runtime API)
   libtrlm_host.so     standalone host runtime (allocator, tensors, nodes,
                       PCG, scalar maths, RoPE tables) for use without the
                       reference's own runtime objects
@@ -45,7 +46,7 @@ def build_host():
 
 def build_hip_lib():
     srcs = [os.path.join(CSRC, f) for f in ("hip_backend.c", "trlm_gemm.c", "gpu_train.c", "gpu_decode.c", "checkpoint.c",
-                                            "gpu_ops.c")]
+                                            "train_loop.c", "gpu_ops.c")]
     # Host-runtime symbols (allocator_alloc, tensor_*, pcg_*, m_*, rope_build_tables)
     # stay undefined: the reference's objects or libtrlm_host.so provide them.
     _run(["gcc"] + CFLAGS + ["-shared"] + srcs +

@@ -1,6 +1,7 @@
 /* gpu_internal.h -- pieces of the GPU trainer (gpu_train.c) that the KV-cache
- * decoder (gpu_decode.c) reuses.  Not part of the C ABI: every symbol here has
- * hidden visibility in libtrlm_hip.so. */
+ * decoder (gpu_decode.c) and the queued driver loop (train_loop.c) reuse.
+ * Not part of the C ABI: every symbol here has hidden visibility in
+ * libtrlm_hip.so. */
 #ifndef TRLM_GPU_INTERNAL_H
 #define TRLM_GPU_INTERNAL_H
 
@@ -31,6 +32,14 @@ void trlm_gemm_rows(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr
 void trlm_swiglu_rows(GpuTrainer* g, hipDeviceptr_t gu, hipDeviceptr_t h, u32 rows);
 void trlm_embed_rows(GpuTrainer* g, hipDeviceptr_t ids, hipDeviceptr_t x, u32 rows);
 void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hipDeviceptr_t out);
+
+/* Queued driver steps (train_loop.c): see gpu_train.c. */
+void trlm_check_ids(const GpuTrainer* g, const u32* ids, const char* what);
+u32 trlm_embed_groups(GpuTrainer* g, const u32* ids, u32* order, u32* seg);
+void trlm_train_step_queued(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay, f64 clip, hipDeviceptr_t loss_out,
+                            hipDeviceptr_t norm_out, hipDeviceptr_t scale_buf);
+void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc);
+void trlm_eval_queued(GpuTrainer* g, hipDeviceptr_t sum, i32 acc);
 
 #pragma GCC visibility pop
 

@@ -242,6 +242,9 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.argmax_rows = hip_get_kernel(c, "k_argmax_rows");
     g.k.sumsq_partial = hip_get_kernel(c, "k_sumsq_partial");
     g.k.adam = hip_get_kernel(c, "k_adam");
+    g.k.loss_mean = hip_get_kernel(c, "k_loss_mean");
+    g.k.norm_clip = hip_get_kernel(c, "k_norm_clip");
+    g.k.adam_ds = hip_get_kernel(c, "k_adam_ds");
     char name[64];
     snprintf(name, sizeof(name), "k_attn_fwd_hd%u", g.hd);
     g.k.attn_fwd = hip_get_kernel(c, name);
@@ -322,11 +325,12 @@ void gpu_trainer_sample_batch(const u32* tokens, u64 num_tokens, u32 seq_len, u3
 /* Stable counting sort of the rows by token id: rows of one token form a
  * segment, listed in ascending row order (the order in which the reference
  * adds them, embedding.c:10-14). */
-static void embed_segments(GpuTrainer* g, const u32* ids) {
+/* Rows of the batch grouped by token for the embedding backward: order[N]
+ * (row indices, stable within a token) and seg = seg_start[nseg+1] then
+ * seg_tok[nseg]; returns nseg. */
+u32 trlm_embed_groups(GpuTrainer* g, const u32* ids, u32* order, u32* seg) {
     u32 N = g->N, V = g->V;
-    u32* order = g->host_emb;
-    u32* seg = order + N;            /* seg_start[nseg+1] then seg_tok[nseg] */
-    u32* count = seg + 2 * N + 1;    /* [V+1] */
+    u32* count = g->host_emb + 3 * N + 1;    /* [V+1] */
     memset(count, 0, ((u64)V + 1) * sizeof(u32));
     for (u32 n = 0; n < N; n++) {
         if (ids[n] >= V) fatal("token id outside the vocabulary");
@@ -344,13 +348,20 @@ static void embed_segments(GpuTrainer* g, const u32* ids) {
     }
     seg_start[nseg] = N;
     for (u32 n = 0; n < N; n++) order[count[ids[n]]++] = n;
+    return nseg;
+}
+
+static void embed_segments(GpuTrainer* g, const u32* ids) {
+    u32* order = g->host_emb;
+    u32* seg = order + g->N;
+    u32 nseg = trlm_embed_groups(g, ids, order, seg);
     g->emb_nseg = nseg;
-    hip_h2d(g->emb_order, order, (u64)N * sizeof(u32));
+    hip_h2d(g->emb_order, order, (u64)g->N * sizeof(u32));
     hip_h2d(g->emb_seg, seg, (2ull * nseg + 1) * sizeof(u32));
 }
 
 /* Embedding, L blocks, final norm, tied head (model/gpu_train.c:312-378). */
-static void check_ids(const GpuTrainer* g, const u32* ids, const char* what) {
+void trlm_check_ids(const GpuTrainer* g, const u32* ids, const char* what) {
     for (u32 n = 0; n < g->N; n++)
         if (ids[n] >= g->V) {
             fprintf(stderr, "[HIP ERROR] gpu_train: %s[%u] = %u is outside the vocabulary (%u)\n", what, n, ids[n],
@@ -361,11 +372,14 @@ static void check_ids(const GpuTrainer* g, const u32* ids, const char* what) {
 }
 
 /* Embedding, the L blocks and the final norm (-> g->nf).  hook (if any) runs
- * after each layer's QKV projection and RoPE, with that layer's qkv. */
+ * after each layer's QKV projection and RoPE, with that layer's qkv.  ids
+ * NULL: the batch's ids are already in g->ids. */
 void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void* hook_ctx) {
     i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F;
-    check_ids(g, ids, "ids");
-    hip_h2d(g->ids, ids, (u64)N * sizeof(u32));
+    if (ids) {
+        trlm_check_ids(g, ids, "ids");
+        hip_h2d(g->ids, ids, (u64)N * sizeof(u32));
+    }
     {
         hipDeviceptr_t E = P_(g, 0), idp = g->ids, x0 = g->layers[0].x_in;
         void* args[] = { &E, &idp, &x0, &N, &D };
@@ -411,9 +425,12 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
     gemm1(g, GEMM_NT, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 0.0f, NULL, NULL);
 }
 
+/* targets NULL: already in g->targets. */
 static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
-    check_ids(g, targets, "targets");
-    hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
+    if (targets) {
+        trlm_check_ids(g, targets, "targets");
+        hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
+    }
     hipDeviceptr_t lg = g->logits, tg = g->targets, lr = g->loss_rows;
     i32 ld = (i32)g->ldv, V = (i32)g->V;
     f32 grad_scale = 1.0f / (f32)g->N;
@@ -542,6 +559,56 @@ void gpu_trainer_adam_step(GpuTrainer* g, AdamOptimizer* opt) { gpu_trainer_adam
 
 void gpu_trainer_adam_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 grad_scale) {
     adam_launch(g, opt, grad_scale, 0.0f);
+}
+
+/* ---------------- queued driver steps (train_loop.c) ---------------- */
+
+/* One training step of the driver loop with the batch already on the device
+ * (g->ids, g->targets, g->emb_order/emb_seg, g->emb_nseg): forward, CE,
+ * backward, the loss mean into loss_out (f32), the grad norm into norm_out
+ * (f64) and the clip scale into scale_buf (f32), then Adam/AdamW with that
+ * scale.  Nothing waits for the device. */
+void trlm_train_step_queued(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay, f64 clip, hipDeviceptr_t loss_out,
+                            hipDeviceptr_t norm_out, hipDeviceptr_t scale_buf) {
+    forward_to_logits(g, NULL);
+    cross_entropy(g, NULL, 1);
+    backward_pass(g);
+    trlm_loss_mean_queued(g, loss_out, 0);
+    {
+        hipDeviceptr_t x = g->grads, part = g->norm_partial;
+        long long n = (long long)g->total_scalars;
+        void* args[] = { &x, &n, &part };
+        hip_launch(g->k.sumsq_partial, GPU_TRAIN_NORM_BLOCKS, 1, 1, 256, 1, 1, 0, args);
+        i32 np = (i32)GPU_TRAIN_NORM_BLOCKS;
+        void* args2[] = { &part, &np, &clip, &norm_out, &scale_buf };
+        hip_launch(g->k.norm_clip, 1, 1, 1, 64, 1, 1, 0, args2);
+    }
+    opt->t++;
+    f32 bc1 = 1.0f - m_powf(opt->beta1, (f32)opt->t);
+    f32 bc2 = 1.0f - m_powf(opt->beta2, (f32)opt->t);
+    hipDeviceptr_t p = g->params, gr = g->grads, m = g->adam_m, v = g->adam_v;
+    long long n = (long long)g->total_scalars;
+    f32 lr = opt->lr, b1 = opt->beta1, b2 = opt->beta2, eps = opt->eps;
+    f32 lrwd = lr * weight_decay;
+    void* args[] = { &p, &gr, &m, &v, &n, &lr, &b1, &b2, &eps, &bc1, &bc2, &scale_buf, &lrwd };
+    u32 blocks = cdiv_u64((u64)(n / 4) > 0 ? (u64)(n / 4) : 1, 256);
+    hip_launch(g->k.adam_ds, blocks, 1, 1, 256, 1, 1, 0, args);
+}
+
+/* mean_loss of g->loss_rows on the device into *out (acc: added onto it). */
+void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc) {
+    hipDeviceptr_t rows = g->loss_rows;
+    i32 B = (i32)g->B, T = (i32)g->T;
+    void* args[] = { &rows, &B, &T, &out, &acc };
+    hip_launch(g->k.loss_mean, 1, 1, 1, 256, 1, 1, g->B * (u32)sizeof(f32), args);
+}
+
+/* eval_loss with the batch already on the device; the loss is added onto
+ * *sum (acc = 0 starts the sum). */
+void trlm_eval_queued(GpuTrainer* g, hipDeviceptr_t sum, i32 acc) {
+    forward_to_logits(g, NULL);
+    cross_entropy(g, NULL, 1);
+    trlm_loss_mean_queued(g, sum, acc);
 }
 
 /* ---------------- additive entry points (trlm_ext.h) ---------------- */

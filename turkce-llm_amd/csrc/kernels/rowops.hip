@@ -521,9 +521,9 @@ __device__ __forceinline__ void adam_one(float& p, float g, float& m, float& v, 
     p = p - upd;
 }
 
-extern "C" __global__ void __launch_bounds__(256)
-k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, long long n,
-       float lr, float b1, float b2, float eps, float bc1, float bc2, float grad_scale, float lrwd) {
+__device__ __forceinline__ void adam_body(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m,
+                                          float* __restrict__ v, long long n, float lr, float b1, float b2, float eps,
+                                          float bc1, float bc2, float grad_scale, float lrwd) {
     long long q = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     long long nq = n >> 2;
     if (q < nq) {
@@ -542,4 +542,88 @@ k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m
         adam_one(a, g[tail], b, c, lr, b1, b2, eps, bc1, bc2, grad_scale, lrwd);
         p[tail] = a; m[tail] = b; v[tail] = c;
     }
+}
+
+extern "C" __global__ void __launch_bounds__(256)
+k_adam(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v, long long n,
+       float lr, float b1, float b2, float eps, float bc1, float bc2, float grad_scale, float lrwd) {
+    adam_body(p, g, m, v, n, lr, b1, b2, eps, bc1, bc2, grad_scale, lrwd);
+}
+
+// Same step with the gradient scale read from device memory (the clip scale
+// k_norm_clip leaves there), so a queued training step needs no host value.
+extern "C" __global__ void __launch_bounds__(256)
+k_adam_ds(float* __restrict__ p, const float* __restrict__ g, float* __restrict__ m, float* __restrict__ v,
+          long long n, float lr, float b1, float b2, float eps, float bc1, float bc2,
+          const float* __restrict__ grad_scale, float lrwd) {
+    adam_body(p, g, m, v, n, lr, b1, b2, eps, bc1, bc2, *grad_scale, lrwd);
+}
+
+// ------------------------------------------------------- queued driver steps
+// mean_loss (model/gpu_train.c:478-487) on the device: sequence b's T row
+// losses are added in order in f32 and divided by T, then the B means are
+// added in order and divided by B -- the host function's operation sequence.
+// acc != 0 adds the result onto *out (the validation sum over batches,
+// training/train_lm_gpu.c:241-253); otherwise it is stored.  Dynamic LDS:
+// B floats.
+extern "C" __global__ void __launch_bounds__(256)
+k_loss_mean(const float* __restrict__ rows, int B, int T, float* __restrict__ out, int acc) {
+#pragma clang fp contract(off)
+    extern __shared__ float seq_mean[];
+    for (int b = threadIdx.x; b < B; b += blockDim.x) {
+        const float* r = rows + (long long)b * T;
+        float s = 0.f;
+        for (int t = 0; t < T; t++) s += r[t];
+        seq_mean[b] = s / (float)T;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        float sum = 0.f;
+        for (int b = 0; b < B; b++) sum += seq_mean[b];
+        const float mean = sum / (float)B;
+        *out = (acc ? *out : 0.0f) + mean;
+    }
+}
+
+// m_sqrt (runtime/mathlib.c:56-83), the reference's own method: x = m*2^e
+// with m in [1,2), e made even, six Newton steps y = (y + m/y)/2 from
+// m/2 + 1/2, then y*2^(e/2) through the exponent field (no denormals).
+__device__ double ref_sqrt64(double x) {
+#pragma clang fp contract(off)
+    if (x < 0.0) return __longlong_as_double(0x7FF8000000000000ll);
+    const unsigned long long b = (unsigned long long)__double_as_longlong(x);
+    const int ex = (int)((b >> 52) & 0x7FF);
+    if (x == 0.0 || ex == 0x7FF) return x;
+    int e = ex - 1023;
+    double m = __longlong_as_double((long long)((b & 0xFFFFFFFFFFFFFull) | (1023ull << 52)));
+    if (e & 1) { m *= 2.0; e -= 1; }
+    double y = m * 0.5 + 0.5;
+    for (int i = 0; i < 6; i++) y = 0.5 * (y + m / y);
+    const unsigned long long yb = (unsigned long long)__double_as_longlong(y);
+    const long long ne = (long long)((yb >> 52) & 0x7FF) + e / 2;
+    if (ne >= 0x7FF) return __longlong_as_double(0x7FF0000000000000ll);
+    if (ne <= 0) return 0.0;
+    return __longlong_as_double((long long)((yb & 0x800FFFFFFFFFFFFFull) | ((unsigned long long)ne << 52)));
+}
+
+// Grad norm (model/gpu_train.c:502-512: the fixed-grid partial sums added in
+// block order in f64, then m_sqrt) and the driver's clip scale
+// (training/train_lm_gpu.c:218-220: clip/norm in f64, rounded to f32, when
+// the norm exceeds clip; 1 otherwise; clip <= 0 never clips).  One thread.
+extern "C" __global__ void k_norm_clip(const float* __restrict__ partial, int n, double clip,
+                                       double* __restrict__ norm_out, float* __restrict__ scale_out) {
+#pragma clang fp contract(off)
+    if (threadIdx.x != 0) return;
+    double ss = 0.0;
+    for (int i = 0; i < n; i++) ss += (double)partial[i];
+    const double nrm = ref_sqrt64(ss);
+    *norm_out = nrm;
+    *scale_out = (clip > 0.0 && nrm > clip) ? (float)(clip / nrm) : 1.0f;
+}
+
+// Element-wise ref_sqrt64 of n values (lets a host test compare the device
+// restatement with the host runtime's m_sqrt).
+extern "C" __global__ void k_ref_sqrt64(const double* __restrict__ x, double* __restrict__ y, int n) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) y[i] = ref_sqrt64(x[i]);
 }

@@ -86,6 +86,14 @@ class TrlmTimer(C.Structure):
     _fields_ = [("start", C.c_void_p), ("stop", C.c_void_p)]
 
 
+class TrlmSchedule(C.Structure):
+    """Mirror of TrlmSchedule (trlm_ext.h): the driver loop's lr schedule,
+    clip, weight decay and batch seed base."""
+    _fields_ = [("warmup_steps", C.c_uint64), ("total_steps", C.c_uint64), ("peak_lr", C.c_float),
+                ("min_lr", C.c_float), ("grad_clip", C.c_double), ("weight_decay", C.c_float),
+                ("seed_base", C.c_uint64)]
+
+
 _libs = None
 
 
@@ -166,6 +174,11 @@ def _bind(host, hip):
     ckpt_args = [GP, C.c_char_p, C.POINTER(NodeP), C.POINTER(AdamOptimizer)]
     _sig(hip, "gpu_trainer_checkpoint_save", C.c_uint32, ckpt_args)
     _sig(hip, "gpu_trainer_checkpoint_load", C.c_uint32, ckpt_args)
+    _sig(hip, "gpu_trainer_train_steps", None, [GP, C.POINTER(AdamOptimizer), u32p, C.c_uint64,
+                                                C.POINTER(TrlmSchedule), C.c_uint64, C.c_uint32, C.c_void_p,
+                                                C.c_void_p, C.c_void_p])
+    _sig(hip, "gpu_trainer_eval_windows", C.c_float, [GP, u32p, C.c_uint64, C.c_uint64, C.c_uint32])
+    _sig(hip, "trlm_lr_warmup_cosine", C.c_float, [C.c_uint64, C.c_uint64, C.c_uint64, C.c_float, C.c_float])
     DP = C.c_void_p
     f32p = np.ctypeslib.ndpointer(np.float32, flags="C_CONTIGUOUS")
     _sig(hip, "gpu_decoder_create", DP, [GP, C.c_uint32, C.c_uint32])
@@ -384,6 +397,22 @@ class Trainer:
     def checkpoint_load(self, path, adam=None):
         return bool(self.hip.gpu_trainer_checkpoint_load(C.byref(self.g), path.encode(), self.hm.nodes,
                                                          C.byref(adam.opt) if adam else None))
+
+    def train_steps(self, adam, tokens, schedule, first_step, n_steps):
+        """Steps first_step .. first_step+n_steps-1 of the driver loop;
+        returns (losses f32[n], grad_norms f64[n], lrs f32[n])."""
+        losses = np.zeros(n_steps, np.float32)
+        norms = np.zeros(n_steps, np.float64)
+        lrs = np.zeros(n_steps, np.float32)
+        tok = _u32(tokens)
+        self.hip.gpu_trainer_train_steps(C.byref(self.g), C.byref(adam.opt), tok, tok.size, C.byref(schedule),
+                                         first_step, n_steps, losses.ctypes.data, norms.ctypes.data,
+                                         lrs.ctypes.data)
+        return losses, norms, lrs
+
+    def eval_windows(self, tokens, train_tokens, val_tokens, val_batches):
+        return np.float32(self.hip.gpu_trainer_eval_windows(C.byref(self.g), _u32(tokens), train_tokens,
+                                                            val_tokens, val_batches))
 
     def forward_logits(self, ids):
         out = np.zeros((self.B * self.T, self.hm.V), np.float32)
