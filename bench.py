@@ -197,6 +197,44 @@ def driver_benchmarks(trlm, tr, adam, rng, steps, warmup):
             "driver_step_ms_call_sequence": seq * 1e3, "driver_loss_last": float(losses[-1])}
 
 
+def hybrid_benchmarks(trlm, reps=10):
+    """The hybrid path's tied LM head as generate.c runs it each token
+    (lm_forward over a 128-token window: node_matmul2d_gpu of x [128, D] by
+    the transposed view of E [V, D]), with E uploaded on every call (the
+    reference's behaviour) and with E pinned (gpu_ops_pin)."""
+    import ctypes as C
+    host, hip = trlm.libs()
+    alloc = host.allocator_create(1 << 31)
+    hip.gpu_ops_init(C.byref(alloc), trlm.KERNELS.encode())
+    rng = np.random.default_rng(13)
+    Tw = 128
+
+    def leaf(arr):
+        sh = (C.c_uint64 * 2)(*arr.shape)
+        t = host.tensor_create(C.byref(alloc), sh, 2)
+        trlm.tensor_np(t)[:] = arr.ravel()
+        return host.node_leaf(C.byref(alloc), t, 1)
+
+    try:
+        nx = leaf(rng.standard_normal((Tw, D)).astype(np.float32))
+        nE = leaf((0.02 * rng.standard_normal((V, D))).astype(np.float32))
+        nEt = host.node_leaf(C.byref(alloc), host.tensor_transpose(C.byref(nE.contents.value), 0, 1), 1)
+        out = {}
+        for key in ("hybrid_head_ms", "hybrid_head_ms_pinned"):
+            if key.endswith("pinned"):
+                hip.gpu_ops_pin(C.cast(nE.contents.value.data, C.c_void_p).value, V * D)
+            hip.node_matmul2d_gpu(C.byref(alloc), nx, nEt)
+            t0 = time.perf_counter()
+            for _ in range(reps):
+                hip.node_matmul2d_gpu(C.byref(alloc), nx, nEt)
+            out[key] = (time.perf_counter() - t0) / reps * 1e3
+        out["hybrid_head_config"] = "node_matmul2d_gpu [128,384] x E^T [384,31769] view, logits to host"
+        return out
+    finally:
+        hip.gpu_ops_shutdown()
+        host.allocator_destroy(C.byref(alloc))
+
+
 DEC_B, DEC_PROMPT, DEC_CTX = 64, 128, 1024
 
 
@@ -496,6 +534,9 @@ def main():
         log("model: forward / train at B=%d T=%d" % (B, T))
         line.update({k: (round(v, 3) if isinstance(v, float) else v)
                      for k, v in model_benchmarks(trlm, max(3, args.steps // 2), args.warmup).items()})
+    if not args.no_model:
+        log("hybrid path: tied head per generated token")
+        line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in hybrid_benchmarks(trlm).items()})
     if not args.no_model and not args.no_decode:
         log("decode: config 5")
         line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode_benchmark(trlm).items()})

@@ -132,6 +132,18 @@ f32 gpu_trainer_eval_windows(GpuTrainer* g, const u32* tokens, u64 train_tokens,
  * warmup steps, then half a cosine from peak to min by total_steps. */
 f32 trlm_lr_warmup_cosine(u64 step, u64 warmup_steps, u64 total_steps, f32 peak_lr, f32 min_lr);
 
+/* ---- node_matmul2d_gpu operand pinning (gpu_ops.h path) ----
+ * gpu_ops_pin(data, count): the caller promises that data[0..count) stays
+ * unchanged until gpu_ops_unpin_all().  A matmul operand (plain, transposed
+ * or column-sliced view) lying wholly inside a pinned range is then read
+ * from a device copy, made once per GPU on first use, instead of being
+ * uploaded on every call -- for generate/chat, pin every parameter after
+ * loading the model.  Results are unchanged.  gpu_ops_unpin_all frees the
+ * copies; it must not run concurrently with matmuls; gpu_ops_shutdown calls
+ * it. */
+void gpu_ops_pin(const f32* data, u64 count);
+void gpu_ops_unpin_all(void);
+
 /* Stream-event timing on the current context's stream. */
 typedef struct TrlmTimer { hipEvent_t start, stop; } TrlmTimer;
 void trlm_timer_create(TrlmTimer* t);

@@ -9,7 +9,13 @@ GPU matmul node, as tests/test_gpu_ops.c and test_cuda.c exercise it.
   - central-difference gradient check on a 2x3 @ 3x2 product
     (test_gpu_ops.c:52-104);
   - per-worker slots from several threads (gpu_ops_init_workers +
-    gpu_ops_set_worker_id) give the same results; debug counters count calls.
+    gpu_ops_set_worker_id) give the same results; debug counters count calls;
+  - pinned operands (gpu_ops_pin, additive): a product over pinned weights,
+    plain or as the head's transposed view, is bit-identical to the unpinned
+    product; the pinned copy is what is read (changing the host values after
+    pinning leaves the result unchanged until gpu_ops_unpin_all); a view that
+    reaches past a pinned range is uploaded as before; worker slots on the
+    same device share the copy.
 """
 import ctypes as C
 import threading
@@ -167,3 +173,64 @@ def test_worker_slots_from_threads(trlm, orc, ops):
     secs, calls = C.c_double(), C.c_uint32()
     hip.gpu_ops_debug_stats(C.byref(secs), C.byref(calls))
     assert calls.value == 3 and secs.value > 0.0
+
+
+def _data_ptr(node):
+    return C.cast(node.contents.value.data, C.c_void_p).value
+
+
+def test_pinned_operands(trlm, orc, ops):
+    host, hip, alloc = ops
+    rng = np.random.default_rng(9)
+    V, D, T = 2003, 384, 5
+    x = rng.standard_normal((T, D)).astype(np.float32)
+    E = (0.02 * rng.standard_normal((V, D))).astype(np.float32)
+    W = rng.standard_normal((D, 640)).astype(np.float32)
+    nx, nE, nW = leaf(trlm, host, alloc, x), leaf(trlm, host, alloc, E), leaf(trlm, host, alloc, W)
+    Et = host.tensor_transpose(C.byref(nE.contents.value), 0, 1)
+    nEt = host.node_leaf(C.byref(alloc), Et, 1)
+    head0 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nEt))
+    proj0 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nW))
+    try:
+        hip.gpu_ops_pin(_data_ptr(nE), V * D)
+        hip.gpu_ops_pin(_data_ptr(nW), D * 640)
+        head1 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nEt))
+        proj1 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nW))
+        assert np.array_equal(head0.view(np.uint32), head1.view(np.uint32))
+        assert np.array_equal(proj0.view(np.uint32), proj1.view(np.uint32))
+        # the device copy is what is read: host changes are not seen while pinned
+        trlm.tensor_np(nW.contents.value)[:] *= 2.0
+        proj2 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nW))
+        assert np.array_equal(proj0.view(np.uint32), proj2.view(np.uint32))
+        # a view past the pinned range (here: rows 0..D of a longer buffer
+        # whose pin covers only half of it) is uploaded as before
+        hip.gpu_ops_unpin_all()
+        hip.gpu_ops_pin(_data_ptr(nW), (D // 2) * 640)
+        proj3 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nW))
+        want3 = orc.matmul(x, 2.0 * W)
+        assert np.abs(proj3 - want3).max() <= 1e-4 * np.abs(want3).max()
+        # worker slots read the pinned copy too
+        hip.gpu_ops_unpin_all()
+        hip.gpu_ops_pin(_data_ptr(nE), V * D)
+        outs = [None] * 3
+        lock = threading.Lock()
+
+        def work(i):
+            hip.gpu_ops_set_worker_id(i)
+            with lock:
+                outs[i] = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nEt))
+
+        th = [threading.Thread(target=work, args=(i,)) for i in range(3)]
+        for t in th:
+            t.start()
+        for t in th:
+            t.join()
+        for o in outs:
+            assert np.array_equal(o.view(np.uint32), head0.view(np.uint32))
+    finally:
+        hip.gpu_ops_unpin_all()
+        hip.gpu_ops_set_worker_id(-1)
+    # unpinned again: the doubled host values are read
+    proj4 = value(trlm, hip.node_matmul2d_gpu(C.byref(alloc), nx, nW))
+    want4 = orc.matmul(x, 2.0 * W)
+    assert np.abs(proj4 - want4).max() <= 1e-4 * np.abs(want4).max()

@@ -11,7 +11,11 @@
  *   - row-major views with a wider row stride (column slices) are uploaded
  *     with one pitched copy and used with their leading dimension;
  *   - each slot owns a stream and grow-only device buffers (as the
- *     reference's persistent buffers, gpu_ops.c:85-108).
+ *     reference's persistent buffers, gpu_ops.c:85-108);
+ *   - operands inside a range the caller pinned (gpu_ops_pin, trlm_ext.h:
+ *     weights that stay fixed while generate/chat run) are read from a
+ *     device copy made once per GPU, with the view's own leading dimension,
+ *     instead of being uploaded on every call.
  */
 #include <pthread.h>
 #include <stdint.h>
@@ -33,6 +37,20 @@ typedef struct Slot {
 } Slot;
 
 static Slot g_slots[MAX_GPU_CONTEXTS];
+
+/* Pinned host ranges and their device copies (one per device, made on first
+ * use there by the slot that needed it). */
+#define MAX_PINS 4096
+#define MAX_PIN_DEVICES 16
+typedef struct Pin {
+    const f32* data;
+    u64 count;
+    hipDeviceptr_t dev[MAX_PIN_DEVICES];
+    u32 owner[MAX_PIN_DEVICES];     /* slot whose context allocated dev[d] */
+} Pin;
+static Pin g_pins[MAX_PINS];
+static u32 g_num_pins = 0;
+static pthread_mutex_t g_pin_mutex = PTHREAD_MUTEX_INITIALIZER;
 static u32 g_num_worker_slots = 0;
 static int g_initialized = 0;
 static pthread_mutex_t g_slot0_mutex = PTHREAD_MUTEX_INITIALIZER;
@@ -92,8 +110,59 @@ static void slot_release(u32 s) {
     hip_shutdown(&g_slots[s].ctx);
 }
 
+void gpu_ops_pin(const f32* data, u64 count) {
+    if (!data || count == 0) return;
+    pthread_mutex_lock(&g_pin_mutex);
+    if (g_num_pins == MAX_PINS) {
+        fprintf(stderr, "[HIP ERROR] gpu_ops: more than %d pinned ranges\n", MAX_PINS);
+        fflush(stderr);
+        _exit(1);
+    }
+    Pin* p = &g_pins[g_num_pins++];
+    memset(p, 0, sizeof(*p));
+    p->data = data;
+    p->count = count;
+    pthread_mutex_unlock(&g_pin_mutex);
+}
+
+void gpu_ops_unpin_all(void) {
+    pthread_mutex_lock(&g_pin_mutex);
+    for (u32 i = 0; i < g_num_pins; i++)
+        for (u32 d = 0; d < MAX_PIN_DEVICES; d++)
+            if (g_pins[i].dev[d]) {
+                hip_set_current(&g_slots[g_pins[i].owner[d]].ctx);
+                hip_free(g_pins[i].dev[d]);
+            }
+    g_num_pins = 0;
+    pthread_mutex_unlock(&g_pin_mutex);
+}
+
+/* Device address of a view lying wholly inside a pinned range, on the
+ * current slot's device (copying the range there on first use); 0 when the
+ * view is not pinned. */
+static hipDeviceptr_t pinned_view(u32 slot, const f32* data, u64 extent) {
+    hipDeviceptr_t out = 0;
+    pthread_mutex_lock(&g_pin_mutex);
+    for (u32 i = 0; i < g_num_pins; i++) {
+        Pin* p = &g_pins[i];
+        if (data < p->data || data + extent > p->data + p->count) continue;
+        i32 d = g_slots[slot].ctx.device;
+        if (d < 0 || d >= MAX_PIN_DEVICES) break;
+        if (!p->dev[d]) {
+            p->dev[d] = hip_alloc(p->count * sizeof(f32));
+            p->owner[d] = slot;
+            hip_h2d(p->dev[d], p->data, p->count * sizeof(f32));
+        }
+        out = (hipDeviceptr_t)((char*)p->dev[d] + (u64)(data - p->data) * sizeof(f32));
+        break;
+    }
+    pthread_mutex_unlock(&g_pin_mutex);
+    return out;
+}
+
 void gpu_ops_shutdown(void) {
     if (!g_initialized) return;
+    gpu_ops_unpin_all();
     slot_release(0);
     for (u32 i = 0; i < g_num_worker_slots; i++) slot_release(1 + i);
     g_num_worker_slots = 0;
@@ -134,11 +203,21 @@ static View classify(Allocator* alloc, const Tensor* t) {
     return v;
 }
 
-/* Upload a view into a packed device buffer (leading dimension = its stored
- * row length) and return that leading dimension. */
-static u64 upload_view(Slot* s, u32 which, const View* v, u64 rows, u64 cols) {
+/* A view's operand on the device: its pinned copy when it lies in a pinned
+ * range (leading dimension as stored on the host), otherwise an upload into
+ * the slot's packed buffer `which` (leading dimension = the stored row
+ * length).  Returns the device pointer; *ld receives the leading dimension. */
+static hipDeviceptr_t upload_view(u32 slot, Slot* s, u32 which, const View* v, u64 rows, u64 cols, u64* ld) {
     u64 srow = v->trans ? rows : cols;      /* stored row length */
     u64 nrow = v->trans ? cols : rows;      /* stored row count  */
+    if (!v->packed.data && nrow > 0 && srow > 0) {
+        hipDeviceptr_t pin = pinned_view(slot, v->data, (nrow - 1) * v->ld + srow);
+        if (pin) {
+            *ld = v->ld;
+            return pin;
+        }
+    }
+    *ld = srow;
     hipDeviceptr_t d = slot_buf(s, which, nrow * srow * sizeof(f32));
     if (v->ld == srow) {
         hip_h2d(d, v->data, nrow * srow * sizeof(f32));
@@ -151,7 +230,7 @@ static u64 upload_view(Slot* s, u32 which, const View* v, u64 rows, u64 cols) {
         }
         hip_sync();
     }
-    return srow;
+    return d;
 }
 
 static Tensor gpu_matmul(Allocator* alloc, const Tensor* a, const Tensor* b) {
@@ -168,10 +247,11 @@ static Tensor gpu_matmul(Allocator* alloc, const Tensor* a, const Tensor* b) {
     Slot* s = &g_slots[slot];
     hip_set_current(&s->ctx);
 
-    u64 lda = upload_view(s, 0, &va, M, K);
-    u64 ldb = upload_view(s, 1, &vb, K, N);
+    u64 lda, ldb;
+    hipDeviceptr_t da = upload_view(slot, s, 0, &va, M, K, &lda);
+    hipDeviceptr_t db = upload_view(slot, s, 1, &vb, K, N, &ldb);
     hipDeviceptr_t dc = slot_buf(s, 2, (M * N > 0 ? M * N : 1) * sizeof(f32));
-    trlm_gemm(s->gemm, va.trans, vb.trans, s->buf[0], s->buf[1], dc, (i32)M, (i32)N, (i32)K, (i32)lda, (i32)ldb,
+    trlm_gemm(s->gemm, va.trans, vb.trans, da, db, dc, (i32)M, (i32)N, (i32)K, (i32)lda, (i32)ldb,
               (i32)N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, (i32)N);
     hip_d2h(out.data, dc, M * N * sizeof(f32));
 

@@ -226,6 +226,8 @@ def _bind(host, hip):
     _sig(hip, "node_matmul2d_gpu", NodeP, [AP, NodeP, NodeP])
     _sig(hip, "gpu_ops_debug_stats", None, [C.POINTER(C.c_double), C.POINTER(C.c_uint32)])
     _sig(hip, "gpu_ops_debug_reset", None, [])
+    _sig(hip, "gpu_ops_pin", None, [C.c_void_p, C.c_uint64])
+    _sig(hip, "gpu_ops_unpin_all", None, [])
 
 
 GpuTrainer = None
