@@ -59,6 +59,18 @@ struct AttTile {
     // tensor; rows >= rlim are zeroed by store(), not here, so that a
     // prefetch does not have to wait for its data.
     __device__ __forceinline__ void load(const float* base, int ld, int r0, int rlim, int col0) {
+        if (r0 + 64 <= rlim) {
+            // whole tile in range: one wave-uniform row base, per-thread
+            // 32-bit offsets
+            const float* b = base + (long long)r0 * ld + col0;
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                int idx = threadIdx.x + i * 256;
+                int r = idx / (HD / 4), c = (idx % (HD / 4)) * 4;
+                v[i] = *(const f32x4*)(b + (r * ld + c));
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             int idx = threadIdx.x + i * 256;
@@ -97,6 +109,16 @@ struct AttTileT {
         c = 4 * (4 * (blk >> 2) + (l >> 4));
     }
     __device__ __forceinline__ void load(const float* base, int ld, int r0, int rlim, int col0) {
+        if (r0 + 64 <= rlim) {
+            const float* b = base + (long long)r0 * ld + col0;
+#pragma unroll
+            for (int i = 0; i < NQ; i++) {
+                int r, c;
+                coords(i, r, c);
+                v[i] = *(const f32x4*)(b + (r * ld + c));
+            }
+            return;
+        }
 #pragma unroll
         for (int i = 0; i < NQ; i++) {
             int r, c;
@@ -245,35 +267,45 @@ __device__ void flash_fwd(const AttnParams& p) {
                 for (int t = 0; t < 4; t++) s[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[j][t], s[c], 0, 0, 0);
             }
         }
-        const bool diag = (kv0 + 63 > qw0);
-        float mx = m;
+        // Causal mask on the diagonal block only (the block index is
+        // wave-uniform); the max is taken on the raw scores (the scale is
+        // positive) and the scale folds into the exponent's FMA.  Every
+        // processed block holds key kv0 <= qpos, so each row has a finite max.
+        if (kv0 + 63 > qw0) {
+#pragma unroll
+            for (int c = 0; c < 2; c++)
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (kpos > qpos) s[c][r] = -INFINITY;
+                }
+        }
+        float mr = s[0][0];
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                float v = s[c][r] * c2;
-                if (diag && kpos > qpos) v = -INFINITY;
-                s[c][r] = v;
-                mx = fmaxf(mx, v);
-            }
-        mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
-        const float alpha = exp2f(m - mx);
+            for (int r = 0; r < 16; r++) mr = fmaxf(mr, s[c][r]);
+        mr = fmaxf(mr, __shfl_xor(mr, 32, WAVE));
+        const float mx = fmaxf(m, mr * c2);
+        const float alpha = __builtin_amdgcn_exp2f(m - mx);
         m = mx;
         float ls = 0.f;
 #pragma unroll
         for (int c = 0; c < 2; c++)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
-                float e = exp2f(s[c][r] - mx);
+                float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][r], c2, -mx));
                 s[c][r] = e;
                 ls += e;
             }
         l = l * alpha + ls;
+        // rescale only when some row's max moved (alpha != 1)
+        if (__ballot(alpha != 1.0f)) {
 #pragma unroll
-        for (int d = 0; d < DB; d++)
+            for (int d = 0; d < DB; d++)
 #pragma unroll
-            for (int r = 0; r < 16; r++) o[d][r] *= alpha;
+                for (int r = 0; r < 16; r++) o[d][r] *= alpha;
+        }
         // O^T += V^T P^T: registers 4g..4g+3 of s[c] hold keys
         // c*32 + 8g + 4*half + (0..3), one 128-bit read of V^T each
 #pragma unroll
@@ -411,13 +443,20 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
                     dp = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], gf[j][t], dp, 0, 0, 0);
                 }
             }
+            // P recomputed from the saved log-sum-exp; the causal mask only on
+            // the diagonal block (wave-uniform test)
+            f32x16 pr;
 #pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                float pr = exp2f(s[r] * c2 - lq);
-                if (kpos > qpos) pr = 0.f;
-                dp[r] = pr * (dp[r] - dq_i) * p.scale;
+            for (int r = 0; r < 16; r++) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -lq));
+            if (kv0 + 63 > qw0) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (kpos > qpos) pr[r] = 0.f;
+                }
             }
+#pragma unroll
+            for (int r = 0; r < 16; r++) dp[r] = pr[r] * (dp[r] - dq_i) * p.scale;
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int kr = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -539,14 +578,24 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
                     dp = __builtin_amdgcn_mfma_f32_32x32x2f32(ga[t], vf[jj][t], dp, 0, 0, 0);
                 }
             }
+            // mask (keys after the query, queries past the end) only where the
+            // block can hold such pairs (wave-uniform test)
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int ql = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                const int qpos = q0 + ql;
-                float pr = exp2f(s[r] * c2 - Ls[ql]);
-                if (kpos > qpos || qpos >= p.T) pr = 0.f;
-                s[r] = pr;
-                dp[r] = pr * (dp[r] - Ds[ql]) * p.scale;
+                s[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -Ls[ql]));
+            }
+            if (q0 < kw0 + 32 || q0 + 64 > p.T) {
+#pragma unroll
+                for (int r = 0; r < 16; r++) {
+                    const int qpos = q0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                    if (kpos > qpos || qpos >= p.T) s[r] = 0.f;
+                }
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                const int ql = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+                dp[r] = s[r] * (dp[r] - Ds[ql]) * p.scale;
             }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
@@ -589,7 +638,9 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
 }
 
 #define ATT_KERNELS(HD)                                                                                   \
-    extern "C" __global__ void __launch_bounds__(256) k_attn_fwd_hd##HD(AttnParams p) { flash_fwd<HD>(p); } \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_fwd_hd##HD(AttnParams p) { \
+        flash_fwd<HD>(p);                                                                                 \
+    }                                                                                                     \
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dkv_hd##HD(AttnParams p) { \
         flash_bwd_dkv<HD>(p);                                                                             \
     }                                                                                                     \
