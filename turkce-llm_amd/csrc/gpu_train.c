@@ -519,10 +519,13 @@ f32 gpu_trainer_forward_backward(GpuTrainer* g, const u32* ids, const u32* targe
     return mean_loss(g);
 }
 
+/* The loss rows come from the CE's statistics pass alone, so eval skips the
+ * gradient pass (the reference's kernel also overwrites the logits with
+ * their gradient here, which no caller can observe): same loss, bit for bit. */
 f32 gpu_trainer_eval_loss(GpuTrainer* g, const u32* ids, const u32* targets) {
     bind(g);
     forward_to_logits(g, ids);
-    cross_entropy(g, targets, 1);
+    cross_entropy(g, targets, 0);
     return mean_loss(g);
 }
 
@@ -607,7 +610,7 @@ void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc) {
  * *sum (acc = 0 starts the sum). */
 void trlm_eval_queued(GpuTrainer* g, hipDeviceptr_t sum, i32 acc) {
     forward_to_logits(g, NULL);
-    cross_entropy(g, NULL, 1);
+    cross_entropy(g, NULL, 0);
     trlm_loss_mean_queued(g, sum, acc);
 }
 
