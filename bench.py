@@ -491,7 +491,7 @@ def main():
         traffic_probe(trlm)
         return
     if args.model_only:
-        print(json.dumps(model_benchmarks(trlm, args.steps, args.warmup)), flush=True)
+        print(json.dumps(model_benchmarks(trlm, args.steps, max(6, args.warmup))), flush=True)
         return
     dev = trlm.Device()
     sweep = Sweep(trlm, dev)
@@ -532,8 +532,9 @@ def main():
     }
     if not args.no_model:
         log("model: forward / train at B=%d T=%d" % (B, T))
+        # the clocks settle over the first few full-model steps: at least 6 untimed
         line.update({k: (round(v, 3) if isinstance(v, float) else v)
-                     for k, v in model_benchmarks(trlm, max(3, args.steps // 2), args.warmup).items()})
+                     for k, v in model_benchmarks(trlm, max(3, args.steps // 2), max(6, args.warmup)).items()})
     if not args.no_model:
         log("hybrid path: tied head per generated token")
         line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in hybrid_benchmarks(trlm).items()})

@@ -74,6 +74,8 @@ typedef struct GpuTrainer {
     u32* host_emb;                            /* [N + 2N + 1 + V + 1] */
     hipDeviceptr_t norm_partial;              /* [GPU_TRAIN_NORM_BLOCKS] */
     f32* host_norm_partial;
+    hipDeviceptr_t ce_stats;                  /* [N][ce_stats_cap] (max, sum) from the LM-head GEMM */
+    i32 ce_stats_cap, ce_nst;
 } GpuTrainer;
 
 GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,

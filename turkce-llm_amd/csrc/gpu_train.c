@@ -192,6 +192,8 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.rf = dalloc(N);
     g.logits = dalloc(N * (u64)g.ldv);
     hip_memset_zero(g.logits, N * (u64)g.ldv * F4);
+    g.ce_stats_cap = 2 * (i32)((g.V + 63) / 64);     /* two entries per 64-wide (smallest) tile column */
+    g.ce_stats = dalloc(N * (u64)g.ce_stats_cap * 2);
 
     g.dres = dalloc(N * D);
     g.dn = dalloc(N * D);
@@ -421,8 +423,10 @@ void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void
 static void forward_to_logits(GpuTrainer* g, const u32* ids) {
     i32 N = (i32)g->N, D = (i32)g->D, V = (i32)g->V, ldv = (i32)g->ldv;
     trlm_forward_hidden(g, ids, NULL, NULL);
-    /* logits = nf @ E^T  (tied head, NT with B = E [V, D]) */
-    gemm1(g, GEMM_NT, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 0.0f, NULL, NULL);
+    /* logits = nf @ E^T  (tied head, NT with B = E [V, D]); the epilogue also
+     * leaves each row's softmax statistics per column block for the CE */
+    g->ce_nst = trlm_gemm_rowstats(g->gemm, 0, 1, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 1, 0, 0, 0, 1.0f,
+                                   0.0f, NULL, NULL, ldv, g->ce_stats, g->ce_stats_cap);
 }
 
 /* targets NULL: already in g->targets. */
@@ -431,10 +435,10 @@ static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
         trlm_check_ids(g, targets, "targets");
         hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
     }
-    hipDeviceptr_t lg = g->logits, tg = g->targets, lr = g->loss_rows;
-    i32 ld = (i32)g->ldv, V = (i32)g->V;
+    hipDeviceptr_t lg = g->logits, tg = g->targets, lr = g->loss_rows, st = g->ce_stats;
+    i32 ld = (i32)g->ldv, V = (i32)g->V, nst = g->ce_nst;
     f32 grad_scale = 1.0f / (f32)g->N;
-    void* args[] = { &lg, &ld, &tg, &lr, &V, &grad_scale, &write_grad };
+    void* args[] = { &lg, &ld, &tg, &lr, &V, &grad_scale, &write_grad, &st, &nst };
     hip_launch(g->k.cross_entropy, g->N, 1, 1, 256, 1, 1, 0, args);
 }
 

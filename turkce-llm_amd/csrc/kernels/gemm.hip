@@ -45,6 +45,8 @@ struct GemmParams {
     int splits, kchunk;
     float alpha, beta;
     int tiles_m, tiles_n;
+    float* stats;      // optional: per-row (max, sum exp(v - max)) of each wave's columns
+    int stats_ld;      // float2 entries per row of stats
 };
 
 __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
@@ -324,6 +326,46 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
     constexpr int FM = BM / 64, FN = BN / 64;
     constexpr int JG = FN < 2 ? FN : 2;
     const int half = lane >> 5, ml = lane & 31;
+    if (p.stats) {
+        // Row statistics for a softmax over the row (the LM head's
+        // cross-entropy): per row, the max of this wave's BN/2 columns of
+        // v = alpha*acc and the sum of exp(v - max); columns >= N are left
+        // out ((-inf, 0) when none is in range).  Entry (row, c0 / (BN/2)) =
+        // (row, 2*tile column + wave column half).  Only for beta = 0 and no
+        // bias / residual (the host asks for it on the LM head only).
+        constexpr float L2E = 1.4426950408889634f;
+        const int sc = c0 / (BN / 2);
+#pragma unroll
+        for (int i = 0; i < FM; i++) {
+            float mx = -INFINITY;
+#pragma unroll
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++)
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (c0 + j * 32 + 8 * g + 4 * half + q < p.N) mx = fmaxf(mx, p.alpha * acc[i][j][4 * g + q]);
+            mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
+            float sm = 0.f;
+            if (mx != -INFINITY) {
+#pragma unroll
+                for (int j = 0; j < FN; j++)
+#pragma unroll
+                    for (int g = 0; g < 4; g++)
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            if (c0 + j * 32 + 8 * g + 4 * half + q < p.N)
+                                sm += __builtin_amdgcn_exp2f((p.alpha * acc[i][j][4 * g + q] - mx) * L2E);
+            }
+            sm += __shfl_xor(sm, 32, WAVE);
+            const int row = r0 + i * 32 + ml;
+            if (half == 0 && row < p.M) {
+                float* st = p.stats + 2 * ((long long)row * p.stats_ld + sc);
+                st[0] = mx;
+                st[1] = sm;
+            }
+        }
+    }
     const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
     const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;
     const bool vec = !(p.beta != 0.f && p.resid) &&

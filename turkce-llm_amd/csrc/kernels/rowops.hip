@@ -386,14 +386,20 @@ __device__ __forceinline__ void ms_combine(float& m, float& s, float m2, float s
 
 extern "C" __global__ void __launch_bounds__(256)
 k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__ targets,
-                float* __restrict__ loss_rows, int V, float grad_scale, int write_grad) {
+                float* __restrict__ loss_rows, int V, float grad_scale, int write_grad,
+                const float* __restrict__ stats, int nst) {
     __shared__ float sm[4], ss[4];
     const long long row = blockIdx.x;
     float* z = logits + row * ld;
     const bool vec = ((ld & 3) == 0);
     float m = -INFINITY, s = 0.f;
     const float L2E = 1.4426950408889634f;
-    if (vec) {
+    if (stats) {
+        // the LM-head GEMM left (max, sum) per column block of the row:
+        // combine them in a fixed order instead of re-reading the logits
+        const float* st = stats + 2 * row * nst;
+        for (int q = threadIdx.x; q < nst; q += 256) ms_combine(m, s, st[2 * q], st[2 * q + 1]);
+    } else if (vec) {
         // per float4: one rescale to the new running max, then four
         // exponentials (exp2 of log2e-scaled differences, one instruction)
         const int nq = (V + 3) >> 2;

@@ -21,7 +21,7 @@
 #include <string.h>
 #include <unistd.h>
 
-#include "trlm_ext.h"
+#include "gpu_internal.h"
 
 /* Kernel argument block; layout identical to struct GemmParams in gemm.hip. */
 typedef struct GemmParams {
@@ -36,6 +36,8 @@ typedef struct GemmParams {
     int splits, kchunk;
     float alpha, beta;
     int tiles_m, tiles_n;
+    float* stats;
+    int stats_ld;
 } GemmParams;
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
@@ -110,6 +112,18 @@ i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits) {
 static int cdiv(long long a, long long b) { return (int)((a + b - 1) / b); }
 
 static int aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+/* Row statistics: 2 entries per tile column (one per wave column half);
+ * the caller's buffer holds stats_cap entries per row. */
+static void set_stats(GemmParams* p, hipDeviceptr_t stats, i32 stats_cap, int bn) {
+    int n = 2 * cdiv(p->N, bn);
+    if (n > stats_cap) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need %d entries per row, buffer has %d\n", n, stats_cap);
+        _exit(1);
+    }
+    p->stats = (float*)stats;
+    p->stats_ld = n;
+}
 
 static void launch(hipFunction_t f, GemmParams* p, u32 gz) {
     void* args[] = { p };
@@ -206,7 +220,19 @@ const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 ba
 void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr) {
-    if (M <= 0 || N <= 0 || batch == 0) return;
+    trlm_gemm_rowstats(e, trans_a, trans_b, A, B, C, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta, bias,
+                       resid, ldr, 0, 0);
+}
+
+i32 trlm_gemm_rowstats(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+                       i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+                       f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr,
+                       hipDeviceptr_t stats, i32 stats_cap) {
+    if (M <= 0 || N <= 0 || batch == 0) return 0;
+    if (stats && (batch != 1 || beta != 0.0f || bias || resid)) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single GEMM with no beta, bias or residual\n");
+        _exit(1);
+    }
     if (M > (1 << 30) || N > (1 << 30) || K < 0) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: bad shape M=%d N=%d K=%d\n", M, N, K);
         _exit(1);
@@ -228,8 +254,9 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
         p.tiles_m = cdiv(M, 64); p.tiles_n = cdiv(N, 64);
         snprintf(e->last, sizeof(e->last), "k_gemm_%s_64x64_u", LAYOUT_NAME[layout]);
         e->last_splits = 1;
+        if (stats) set_stats(&p, stats, stats_cap, 64);
         launch(e->ku[layout], &p, batch);
-        return;
+        return p.stats ? 2 * p.tiles_n : 0;
     }
 
     int tile, splits;
@@ -239,8 +266,10 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
         splits = batch == 1 ? auto_splits(tiles_of(tile, M, N, 1), K) : 1;
     }
     if (e->force_splits > 0 && batch == 1) splits = e->force_splits;
+    if (stats) splits = 1;                 /* statistics need whole sums */
     p.tiles_m = cdiv(M, TILES[tile].bm);
     p.tiles_n = cdiv(N, TILES[tile].bn);
+    if (stats) set_stats(&p, stats, stats_cap, TILES[tile].bn);
     int kchunk = K;
     if (splits > 1 && K < 2 * KCHUNK_ALIGN) splits = 1;
     if (splits > 1) {
@@ -251,7 +280,7 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
     e->last_splits = splits;
     if (splits <= 1) {
         launch(e->k[layout][tile], &p, batch);
-        return;
+        return p.stats ? 2 * p.tiles_n : 0;
     }
     /* split-K: raw partials into the workspace, then an ordered reduction */
     u64 need = (u64)splits * (u64)M * (u64)N;
@@ -274,6 +303,7 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
     i64 sW = (i64)M * N;
     void* args[] = { &W, &sp, &sW, &C, &M, &N, &ldc, &alpha, &beta, &bias, &resid, &ldr };
     hip_launch(e->reduce, (u32)((total + 255) / 256), 1, 1, 256, 1, 1, 0, args);
+    return 0;
 }
 
 void trlm_timer_create(TrlmTimer* t) {
