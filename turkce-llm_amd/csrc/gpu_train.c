@@ -58,6 +58,15 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
               bias, resid, ldc);
 }
 
+/* Weight and bias gradient of a linear layer in one GEMM:
+ * dW [M, N] = X^T @ dY (TN, X [K=rows, M], dY [rows, N]) and db [N] =
+ * column sums of dY, which the GEMM adds up from the dY tiles it loads
+ * (model/gpu_train.c:415-432 runs k_colsum_acc separately). */
+static void gemm_wb(GpuTrainer* g, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW, hipDeviceptr_t db, i32 M,
+                    i32 N, i32 K) {
+    trlm_gemm_ex(g->gemm, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, NULL, 0, db);
+}
+
 /* threads of k_swiglu_fwd / k_swiglu_bwd: one float4 each when F % 4 == 0 */
 static u32 swiglu_blocks(const GpuTrainer* g, u64 rows) {
     u64 work = rows * g->F;
@@ -89,21 +98,6 @@ static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
     hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
     i32 inb = (i32)nb, acc = 0;
     void* args2[] = { &part, &inb, &cols, &dw, &acc };
-    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
-}
-
-#define COLSUM_RPB 16u
-
-/* out[c] = sum_r in[r, c] (bias gradients; the role of colsum_acc,
- * gpu_train.c:120-123) */
-static void colsum(GpuTrainer* g, hipDeviceptr_t in, hipDeviceptr_t out, i32 rows, i32 cols) {
-    hipDeviceptr_t part = g->part;
-    i32 ld = cols, rpb = (i32)COLSUM_RPB;
-    u32 nb = cdiv_u64((u64)rows, COLSUM_RPB);
-    void* args[] = { &in, &rows, &cols, &ld, &rpb, &part };
-    hip_launch(g->k.colsum_partial, nb, 1, 1, 256, 1, 1, 0, args);
-    i32 inb = (i32)nb, acc = 0;
-    void* args2[] = { &part, &inb, &cols, &out, &acc };
     hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
 }
 
@@ -202,11 +196,8 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.dh = dalloc(N * F);
     g.dgu = dalloc(N * 2 * F);
     g.dvec = dalloc(BHT);
-    u64 wide = 3 * D > 2 * F ? 3 * D : 2 * F;
-    u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;
-    u64 part_floats = part_rows * D;
-    if (((N + COLSUM_RPB - 1) / COLSUM_RPB) * wide > part_floats) part_floats = ((N + COLSUM_RPB - 1) / COLSUM_RPB) * wide;
-    g.part = dalloc(part_floats);
+    u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;   /* RMSNorm weight-gradient partials */
+    g.part = dalloc(part_rows * D);
 
     g.ids = hip_alloc(N * sizeof(u32));
     g.targets = hip_alloc(N * sizeof(u32));
@@ -235,7 +226,6 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.embed_bwd = hip_get_kernel(c, "k_embed_bwd");
     g.k.rmsnorm_fwd = hip_get_kernel(c, "k_rmsnorm_fwd");
     g.k.rmsnorm_bwd = hip_get_kernel(c, "k_rmsnorm_bwd");
-    g.k.colsum_partial = hip_get_kernel(c, "k_colsum_partial");
     g.k.colsum_final = hip_get_kernel(c, "k_colsum_final");
     g.k.rope_qk = hip_get_kernel(c, "k_rope_qk");
     g.k.swiglu_fwd = hip_get_kernel(c, "k_swiglu_fwd");
@@ -425,8 +415,8 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
     trlm_forward_hidden(g, ids, NULL, NULL);
     /* logits = nf @ E^T  (tied head, NT with B = E [V, D]); the epilogue also
      * leaves each row's softmax statistics per column block for the CE */
-    g->ce_nst = trlm_gemm_rowstats(g->gemm, 0, 1, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 1, 0, 0, 0, 1.0f,
-                                   0.0f, NULL, NULL, ldv, g->ce_stats, g->ce_stats_cap);
+    g->ce_nst = trlm_gemm_ex(g->gemm, 0, 1, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 1, 0, 0, 0, 1.0f, 0.0f,
+                             NULL, NULL, ldv, g->ce_stats, g->ce_stats_cap, NULL);
 }
 
 /* targets NULL: already in g->targets. */
@@ -460,21 +450,18 @@ static void backward_pass(GpuTrainer* g) {
         GpuLayerActs* a = &g->layers[l];
         u32 ul = (u32)l;
         /* FFN: x3 = x2 + (h @ Wd + bd); dres = dx3 */
-        gemm1(g, GEMM_TN, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), F, D, N, F, D, D, 0.0f, NULL, NULL);
-        colsum(g, g->dres, G_(g, pidx(ul, PK_BDOWN)), N, D);
+        gemm_wb(g, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), G_(g, pidx(ul, PK_BDOWN)), F, D, N);
         gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WDOWN)), g->dh, N, F, D, D, D, F, 0.0f, NULL, NULL);
         {
             hipDeviceptr_t gu = a->gu, dh = g->dh, dgu = g->dgu;
             void* args[] = { &gu, &dh, &dgu, &N, &F };
             hip_launch(g->k.swiglu_bwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);
         }
-        gemm1(g, GEMM_TN, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), D, 2 * F, N, D, 2 * F, 2 * F, 0.0f, NULL, NULL);
-        colsum(g, g->dgu, G_(g, pidx(ul, PK_BGU)), N, 2 * F);
+        gemm_wb(g, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), G_(g, pidx(ul, PK_BGU)), D, 2 * F, N);
         gemm1(g, GEMM_NT, g->dgu, P_(g, pidx(ul, PK_WGU)), g->dn, N, D, 2 * F, 2 * F, 2 * F, D, 0.0f, NULL, NULL);
         rmsnorm_bwd(g, a->x2, P_(g, pidx(ul, PK_FFN_NORM)), a->r2, g->dn, g->dres, G_(g, pidx(ul, PK_FFN_NORM)));
         /* attention: x2 = x + (att @ Wo + bo); dres = dx2 */
-        gemm1(g, GEMM_TN, a->att, g->dres, G_(g, pidx(ul, PK_WO)), D, D, N, D, D, D, 0.0f, NULL, NULL);
-        colsum(g, g->dres, G_(g, pidx(ul, PK_BO)), N, D);
+        gemm_wb(g, a->att, g->dres, G_(g, pidx(ul, PK_WO)), G_(g, pidx(ul, PK_BO)), D, D, N);
         gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
         ap.qkv = (const float*)a->qkv; ap.O = (const float*)a->att; ap.dO = (const float*)g->datt;
         ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
@@ -484,9 +471,7 @@ static void backward_pass(GpuTrainer* g) {
             hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
         rope(g, g->dqkv, 1);
-        gemm1(g, GEMM_TN, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), D, 3 * D, N, D, 3 * D, 3 * D, 0.0f, NULL,
-              NULL);
-        colsum(g, g->dqkv, G_(g, pidx(ul, PK_BQKV)), N, 3 * D);
+        gemm_wb(g, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
         gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,
               NULL);
         rmsnorm_bwd(g, a->x_in, P_(g, pidx(ul, PK_ATTN_NORM)), a->r1, g->dn, g->dres,

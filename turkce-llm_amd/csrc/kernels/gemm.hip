@@ -47,6 +47,8 @@ struct GemmParams {
     int tiles_m, tiles_n;
     float* stats;      // optional: per-row (max, sum exp(v - max)) of each wave's columns
     int stats_ld;      // float2 entries per row of stats
+    float* csum;       // optional (TB = 0): column sums of B over k (a bias gradient);
+                       // with split-K each split writes its partial as row M of its slab
 };
 
 __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
@@ -174,10 +176,20 @@ struct TileStream {
     }
 };
 
+// Column sums of B over k (TB = 0): every thread's B loads fall on the same
+// four columns, so it keeps one f32x4 of running sums, added at the tile
+// stores; the end of gemm_body adds up the threads of each column.
+template <int BN, int BK, int NLB>
+__device__ __forceinline__ void colsum_add(f32x4& cs, const f32x4 (&rb)[NLB]) {
+#pragma unroll
+    for (int i = 0; i < NLB; i++) cs += rb[i];
+}
+
 // Edge tiles and the scalar-load variants: every load checked.
 template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
 __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* A, const float* B, int m0, int n0,
-                                              int kb, int ke, float* lds, f32x16 (&acc)[BM / 64][BN / 64]) {
+                                              int kb, int ke, float* lds, f32x16 (&acc)[BM / 64][BN / 64],
+                                              bool cs_on, f32x4& cs) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -195,6 +207,7 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* 
     auto lstore = [&](int buf) {
         store_tile<BM, BK, AK>(lds + buf * (ASZ + BSZ), ra);
         store_tile<BN, BK, BK_>(lds + buf * (ASZ + BSZ) + ASZ, rb);
+        if (!BK_ && cs_on) colsum_add<BN, BK, (NLB > 0 ? NLB : 1)>(cs, rb);
     };
 
     const int nk = (ke - kb + BK - 1) / BK;
@@ -240,7 +253,7 @@ __device__ __forceinline__ void fetch_frags(const float* lds, int rb0, int kk, i
 template <int TA, int TB, int BM, int BN, int BK>
 __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const float* A, const float* B, int m0,
                                                    int n0, int kb, int ke, float* lds,
-                                                   f32x16 (&acc)[BM / 64][BN / 64]) {
+                                                   f32x16 (&acc)[BM / 64][BN / 64], bool cs_on, f32x4& cs) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
     constexpr int WM = BM / 2, WN = BN / 2;
@@ -262,6 +275,7 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
     sb.load(rb);
     store_tile<BM, BK, AK>(lds, ra);
     store_tile<BN, BK, BK_>(lds + ASZ, rb);
+    if (!BK_ && cs_on) colsum_add<BN, BK, NLB>(cs, rb);
     if (nk > 1) {
         sa.load(ra);
         sb.load(rb);
@@ -285,6 +299,7 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
                 if (kt + 1 < nk) {
                     store_tile<BM, BK, AK>(ln, ra);
                     store_tile<BN, BK, BK_>(ln + ASZ, rb);
+                    if (!BK_ && cs_on) colsum_add<BN, BK, NLB>(cs, rb);
                 }
                 __syncthreads();
                 if (kt + 1 < nk) {
@@ -479,11 +494,31 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     // Interior tiles whose k-range is whole BK steps take the pipelined,
     // check-free loop; edge tiles (and the scalar-load variants) the guarded one.
     const bool full = ALIGNED && m0 + BM <= p.M && n0 + BN <= p.N && ke > kb && (ke - kb) % BK == 0;
+    // the first row of tiles also sums B's columns over its k-range
+    const bool cs_on = TB == 0 && p.csum != nullptr && tm == 0;
+    f32x4 cs = {0.f, 0.f, 0.f, 0.f};
     if constexpr (ALIGNED) {
-        if (full) gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc);
-        else gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kb, ke, lds, acc);
+        if (full) gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+        else gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
     } else {
-        gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc);
+        gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+    }
+    if (TB == 0 && cs_on) {
+        // threads t, t + BN/4, ... hold the same four columns: add them in
+        // thread order through LDS (free after the main loop's last barrier)
+        constexpr int G = BN / 4, R = 256 / G;
+        f32x4* xs = reinterpret_cast<f32x4*>(lds);
+        xs[threadIdx.x] = cs;
+        __syncthreads();
+        if (threadIdx.x < G) {
+            f32x4 t = xs[threadIdx.x];
+#pragma unroll
+            for (int j = 1; j < R; j++) t += xs[threadIdx.x + j * G];
+            float* dst = p.splits > 1 ? C + (long long)p.M * p.ldc : p.csum;
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (n0 + 4 * threadIdx.x + e < p.N) dst[n0 + 4 * threadIdx.x + e] = t[e];
+        }
     }
 
     gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
@@ -524,12 +559,17 @@ GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, 16, false, 1)
 extern "C" __global__ void __launch_bounds__(256)
 k_gemm_splitk_reduce(const float* __restrict__ W, int splits, long long sW, float* __restrict__ C, int M, int N,
                      int ldc, float alpha, float beta, const float* __restrict__ bias,
-                     const float* __restrict__ resid, int ldr) {
+                     const float* __restrict__ resid, int ldr, float* __restrict__ csum) {
     long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (long long)M * N) return;
+    const long long rows = M + (csum ? 1 : 0);   // row M: the splits' column-sum partials
+    if (i >= rows * N) return;
     int m = (int)(i / N), n = (int)(i - (long long)m * N);
     float s = W[i];
     for (int k = 1; k < splits; k++) s += W[k * sW + i];
+    if (m == M) {
+        csum[n] = s;
+        return;
+    }
     float v = alpha * s;
     float* dst = C + (long long)m * ldc + n;
     if (beta != 0.f) v = v + beta * *dst;

@@ -195,50 +195,8 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
 }
 
 // ---------------------------------------------------------------- column sums
-// Stage 1: partial[b, c] = sum of in[r, c] over the rpb rows of block b.
-// 256 threads = G row-lanes x C4 float4 column groups (G = 256 / C4 when a
-// row is narrower than 1024 floats): row-lane g adds rows g, g+G, ... in
-// order, then the G sums are added in g order through LDS.  Fixed
-// assignment and order, so the result is reproducible.
-extern "C" __global__ void __launch_bounds__(256)
-k_colsum_partial(const float* __restrict__ in, int rows, int cols, int ld, int rpb, float* __restrict__ partial) {
-    __shared__ f32x4 red[256];
-    const int b = blockIdx.x, t = threadIdx.x;
-    const int r0 = b * rpb;
-    int r1 = r0 + rpb;
-    if (r1 > rows) r1 = rows;
-    if ((cols & 3) == 0 && (ld & 3) == 0) {
-        const int C4 = cols >> 2;
-        if (C4 >= 256) {
-            for (int c4 = t; c4 < C4; c4 += 256) {
-                f32x4 s = {0.f, 0.f, 0.f, 0.f};
-                for (int r = r0; r < r1; r++) s += *(const f32x4*)(in + (long long)r * ld + 4 * c4);
-                *(f32x4*)(partial + (long long)b * cols + 4 * c4) = s;
-            }
-            return;
-        }
-        const int G = 256 / C4;
-        const int c4 = t % C4, g = t / C4;
-        f32x4 s = {0.f, 0.f, 0.f, 0.f};
-        if (g < G)
-            for (int r = r0 + g; r < r1; r += G) s += *(const f32x4*)(in + (long long)r * ld + 4 * c4);
-        red[t] = s;
-        __syncthreads();
-        if (t < C4) {
-            f32x4 acc = red[t];
-            for (int k = 1; k < G; k++) acc += red[k * C4 + t];
-            *(f32x4*)(partial + (long long)b * cols + 4 * t) = acc;
-        }
-        return;
-    }
-    for (int c = t; c < cols; c += 256) {
-        float s = 0.f;
-        for (int r = r0; r < r1; r++) s += in[(long long)r * ld + c];
-        partial[(long long)b * cols + c] = s;
-    }
-}
-
-// Stage 2: out[c] (+)= sum over b of partial[b, c].  A block covers 64
+// out[c] (+)= sum over b of partial[b, c] (the RMSNorm weight gradient's
+// per-block partials).  A block covers 64
 // columns; its 4 wavefronts each add a contiguous quarter of the partial
 // rows in order, and the four quarter sums are added in order.  Loads are
 // issued 16 at a time ahead of their (ordered) additions.

@@ -38,6 +38,7 @@ typedef struct GemmParams {
     int tiles_m, tiles_n;
     float* stats;
     int stats_ld;
+    float* csum;
 } GemmParams;
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
@@ -220,17 +221,21 @@ const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 ba
 void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr) {
-    trlm_gemm_rowstats(e, trans_a, trans_b, A, B, C, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta, bias,
-                       resid, ldr, 0, 0);
+    trlm_gemm_ex(e, trans_a, trans_b, A, B, C, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta, bias, resid,
+                 ldr, 0, 0, 0);
 }
 
-i32 trlm_gemm_rowstats(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
-                       i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
-                       f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr,
-                       hipDeviceptr_t stats, i32 stats_cap) {
+i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+                 i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr,
+                 hipDeviceptr_t stats, i32 stats_cap, hipDeviceptr_t csum) {
     if (M <= 0 || N <= 0 || batch == 0) return 0;
     if (stats && (batch != 1 || beta != 0.0f || bias || resid)) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single GEMM with no beta, bias or residual\n");
+        _exit(1);
+    }
+    if (csum && (batch != 1 || trans_b)) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: column sums need a single GEMM with B stored [K,N]\n");
         _exit(1);
     }
     if (M > (1 << 30) || N > (1 << 30) || K < 0) {
@@ -246,6 +251,7 @@ i32 trlm_gemm_rowstats(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, 
     p.lda = lda; p.ldb = ldb; p.ldc = ldc; p.ldr = ldr;
     p.splits = 1; p.kchunk = K > 0 ? K : 1;
     p.alpha = alpha; p.beta = beta;
+    p.csum = (float*)csum;
 
     int layout = trans_a ? (trans_b ? 3 : L_TN) : (trans_b ? L_NT : L_NN);
     int aligned = layout != 3 && aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
@@ -282,8 +288,10 @@ i32 trlm_gemm_rowstats(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, 
         launch(e->k[layout][tile], &p, batch);
         return p.stats ? 2 * p.tiles_n : 0;
     }
-    /* split-K: raw partials into the workspace, then an ordered reduction */
-    u64 need = (u64)splits * (u64)M * (u64)N;
+    /* split-K: raw partials into the workspace, then an ordered reduction;
+     * with column sums each split's slab has one more row, M, for them */
+    u64 slab = ((u64)M + (csum ? 1u : 0u)) * (u64)N;
+    u64 need = (u64)splits * slab;
     if (need > e->ws_floats) {
         if (e->ws) hip_free(e->ws);
         e->ws = hip_alloc(need * sizeof(f32));
@@ -292,16 +300,16 @@ i32 trlm_gemm_rowstats(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, 
     GemmParams q = p;
     q.C = (float*)e->ws;
     q.ldc = N;
-    q.sW = (long long)M * N;
+    q.sW = (long long)slab;
     q.kchunk = kchunk;
     q.splits = splits;
     q.alpha = 1.0f; q.beta = 0.0f; q.bias = NULL; q.resid = NULL;
     launch(e->k[layout][tile], &q, (u32)splits);
-    long long total = (long long)M * N;
+    long long total = (long long)slab;
     hipDeviceptr_t W = e->ws;
     i32 sp = splits;
-    i64 sW = (i64)M * N;
-    void* args[] = { &W, &sp, &sW, &C, &M, &N, &ldc, &alpha, &beta, &bias, &resid, &ldr };
+    i64 sW = (i64)slab;
+    void* args[] = { &W, &sp, &sW, &C, &M, &N, &ldc, &alpha, &beta, &bias, &resid, &ldr, &csum };
     hip_launch(e->reduce, (u32)((total + 255) / 256), 1, 1, 256, 1, 1, 0, args);
     return 0;
 }
