@@ -42,7 +42,7 @@ typedef struct TrlmGemm TrlmGemm;
 
 typedef struct GpuKernels {
     hipFunction_t fill_zero, embed_fwd, embed_bwd, rmsnorm_fwd, rmsnorm_bwd, colsum_final;
-    hipFunction_t rope_qk, swiglu_fwd, swiglu_bwd, cross_entropy, argmax_rows, sumsq_partial, adam;
+    hipFunction_t swiglu_fwd, swiglu_bwd, cross_entropy, argmax_rows, sumsq_partial, adam;
     hipFunction_t attn_fwd, attn_bwd_dkv, attn_bwd_dq;
     hipFunction_t loss_mean, norm_clip, adam_ds;   /* queued driver steps (trlm_ext.h) */
 } GpuKernels;

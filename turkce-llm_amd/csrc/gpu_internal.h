@@ -33,17 +33,27 @@ void trlm_swiglu_rows(GpuTrainer* g, hipDeviceptr_t gu, hipDeviceptr_t h, u32 ro
 void trlm_embed_rows(GpuTrainer* g, hipDeviceptr_t ids, hipDeviceptr_t x, u32 rows);
 void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hipDeviceptr_t out);
 
-/* trlm_gemm (trlm_ext.h) with two optional by-products:
+/* trlm_gemm (trlm_ext.h) with optional epilogue extras (NULL: none):
  *   stats: per-row softmax statistics of C ([M][stats_cap] float2: (max,
  *          sum exp(v - max)) of each wave's column half of each tile); single
- *          GEMM, beta 0, no bias / residual, no split-K;
+ *          GEMM, beta 0, no bias / residual; no split-K;
  *   csum:  the column sums of op(B) over k ([N]: a bias gradient next to a
- *          weight gradient); single GEMM, B stored [K,N].
+ *          weight gradient); single GEMM, B stored [K,N];
+ *   rope:  columns [0, rope_cols) of C rotated as RoPE pairs of heads of
+ *          rope_hd columns at position row % rope_T (tables [rope_T][rope_hd/2]),
+ *          after bias; single GEMM; no split-K.
  * Returns the stats entries written per row (0 without stats). */
+typedef struct TrlmGemmExtra {
+    hipDeviceptr_t stats;
+    i32 stats_cap;
+    hipDeviceptr_t csum;
+    const f32* rope_cos;
+    const f32* rope_sin;
+    i32 rope_T, rope_hd, rope_cols;
+} TrlmGemmExtra;
 i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
-                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr,
-                 hipDeviceptr_t stats, i32 stats_cap, hipDeviceptr_t csum);
+                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x);
 
 /* Queued driver steps (train_loop.c): see gpu_train.c. */
 void trlm_check_ids(const GpuTrainer* g, const u32* ids, const char* what);

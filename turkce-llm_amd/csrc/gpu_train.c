@@ -64,7 +64,10 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
  * (model/gpu_train.c:415-432 runs k_colsum_acc separately). */
 static void gemm_wb(GpuTrainer* g, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW, hipDeviceptr_t db, i32 M,
                     i32 N, i32 K) {
-    trlm_gemm_ex(g->gemm, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, NULL, 0, db);
+    TrlmGemmExtra x;
+    memset(&x, 0, sizeof(x));
+    x.csum = db;
+    trlm_gemm_ex(g->gemm, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, &x);
 }
 
 /* threads of k_swiglu_fwd / k_swiglu_bwd: one float4 each when F % 4 == 0 */
@@ -112,6 +115,8 @@ typedef struct AttnParams {
     int B, T, H, D;
     int ldq, ldo;
     float scale;
+    const float* rope_cos;
+    const float* rope_sin;
 } AttnParams;
 
 static AttnParams attn_params(GpuTrainer* g) {
@@ -121,13 +126,6 @@ static AttnParams attn_params(GpuTrainer* g) {
     a.ldq = 3 * (int)g->D; a.ldo = (int)g->D;
     a.scale = 1.0f / m_sqrtf((f32)g->hd);   /* attention.c:78 */
     return a;
-}
-
-static void rope(GpuTrainer* g, hipDeviceptr_t qkv, i32 inverse) {
-    hipDeviceptr_t c = g->cos_t, s = g->sin_t;
-    i32 N = (i32)g->N, T = (i32)g->T, H = (i32)g->H, hd = (i32)g->hd, ld = 3 * (i32)g->D;
-    void* args[] = { &qkv, &c, &s, &N, &T, &H, &hd, &ld, &inverse };
-    hip_launch(g->k.rope_qk, cdiv_u64((u64)g->N * g->H * (g->hd / 4), 256), 1, 1, 256, 1, 1, 0, args);
 }
 
 /* ---------------- create / destroy ---------------- */
@@ -227,7 +225,6 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.rmsnorm_fwd = hip_get_kernel(c, "k_rmsnorm_fwd");
     g.k.rmsnorm_bwd = hip_get_kernel(c, "k_rmsnorm_bwd");
     g.k.colsum_final = hip_get_kernel(c, "k_colsum_final");
-    g.k.rope_qk = hip_get_kernel(c, "k_rope_qk");
     g.k.swiglu_fwd = hip_get_kernel(c, "k_swiglu_fwd");
     g.k.swiglu_bwd = hip_get_kernel(c, "k_swiglu_bwd");
     g.k.cross_entropy = hip_get_kernel(c, "k_cross_entropy");
@@ -383,9 +380,19 @@ void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void
         GpuLayerActs* a = &g->layers[l];
         hipDeviceptr_t x_out = (l + 1 < g->L) ? g->layers[l + 1].x_in : g->x_final;
         rmsnorm_fwd(g, a->x_in, P_(g, pidx(l, PK_ATTN_NORM)), a->n1, a->r1);
-        gemm1(g, GEMM_NN, a->n1, P_(g, pidx(l, PK_WQKV)), a->qkv, N, 3 * D, D, D, 3 * D, 3 * D, 0.0f,
-              P_(g, pidx(l, PK_BQKV)), NULL);
-        rope(g, a->qkv, 0);
+        /* qkv = n1 @ Wqkv + b, with RoPE applied to the Q and K columns in
+         * the GEMM's epilogue */
+        {
+            TrlmGemmExtra x;
+            memset(&x, 0, sizeof(x));
+            x.rope_cos = (const f32*)g->cos_t;
+            x.rope_sin = (const f32*)g->sin_t;
+            x.rope_T = (i32)g->T;
+            x.rope_hd = (i32)g->hd;
+            x.rope_cols = 2 * D;
+            trlm_gemm_ex(g->gemm, 0, 0, a->n1, P_(g, pidx(l, PK_WQKV)), a->qkv, N, 3 * D, D, D, 3 * D, 3 * D, 1, 0,
+                         0, 0, 1.0f, 0.0f, P_(g, pidx(l, PK_BQKV)), NULL, 3 * D, &x);
+        }
         if (hook) hook(hook_ctx, g, l, a->qkv);
         ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
         {
@@ -415,8 +422,12 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
     trlm_forward_hidden(g, ids, NULL, NULL);
     /* logits = nf @ E^T  (tied head, NT with B = E [V, D]); the epilogue also
      * leaves each row's softmax statistics per column block for the CE */
+    TrlmGemmExtra x;
+    memset(&x, 0, sizeof(x));
+    x.stats = g->ce_stats;
+    x.stats_cap = g->ce_stats_cap;
     g->ce_nst = trlm_gemm_ex(g->gemm, 0, 1, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 1, 0, 0, 0, 1.0f, 0.0f,
-                             NULL, NULL, ldv, g->ce_stats, g->ce_stats_cap, NULL);
+                             NULL, NULL, ldv, &x);
 }
 
 /* targets NULL: already in g->targets. */
@@ -446,6 +457,8 @@ static void backward_pass(GpuTrainer* g) {
     rmsnorm_bwd(g, g->x_final, P_(g, p_final), g->rf, g->dn, g->dres, G_(g, p_final));
 
     AttnParams ap = attn_params(g);
+    ap.rope_cos = (const float*)g->cos_t;   /* dQ, dK rotated back as they are stored */
+    ap.rope_sin = (const float*)g->sin_t;
     for (i32 l = (i32)g->L - 1; l >= 0; l--) {
         GpuLayerActs* a = &g->layers[l];
         u32 ul = (u32)l;
@@ -470,7 +483,6 @@ static void backward_pass(GpuTrainer* g) {
             hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
             hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
-        rope(g, g->dqkv, 1);
         gemm_wb(g, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
         gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,
               NULL);

@@ -44,6 +44,11 @@ struct AttnParams {
     int B, T, H, D;
     int ldq, ldo;
     float scale;       // 1/sqrt(HD)
+    // backward: when set, dQ and dK leave through the transpose of the RoPE
+    // rotation (tables [T][HD/2]), so dqkv is the gradient of the un-rotated
+    // projection
+    const float* rope_cos;
+    const float* rope_sin;
 };
 
 // One [64 x HD] tile (rows r0.., columns col0.., row stride ld) held in
@@ -169,9 +174,12 @@ __device__ __forceinline__ void att_settle(const f32x4* x) {
 }
 
 // Store a [HD x 32] accumulator set (rows d, one column per lane) to the
-// row of `row` (columns col0 + d): float4 over 4 consecutive d.
+// row of `row` (columns col0 + d): float4 over 4 consecutive d.  With rope
+// tables, the pairs (d0, d0+1), (d0+2, d0+3) are rotated back by position t
+// (the transpose of the forward rotation, model_ops.c:130-155).
 template <int HD>
-__device__ __forceinline__ void att_store_rows(float* rowp, const f32x16* acc, int half, float scale) {
+__device__ __forceinline__ void att_store_rows(float* rowp, const f32x16* acc, int half, float scale,
+                                               const float* rc = nullptr, const float* rs = nullptr, int t = 0) {
     constexpr int DB = (HD + 31) / 32;
 #pragma unroll
     for (int d = 0; d < DB; d++)
@@ -181,6 +189,15 @@ __device__ __forceinline__ void att_store_rows(float* rowp, const f32x16* acc, i
             if (d0 < HD) {
                 f32x4 v = {acc[d][4 * g] * scale, acc[d][4 * g + 1] * scale, acc[d][4 * g + 2] * scale,
                            acc[d][4 * g + 3] * scale};
+                if (rc) {
+                    const int k = t * (HD / 2) + (d0 >> 1);
+                    const float c0 = rc[k], c1 = rc[k + 1], s0 = rs[k], s1 = rs[k + 1];
+                    const f32x4 a = v;
+                    v[0] = a[0] * c0 + a[1] * s0;
+                    v[1] = -a[0] * s0 + a[1] * c0;
+                    v[2] = a[2] * c1 + a[3] * s1;
+                    v[3] = -a[2] * s1 + a[3] * c1;
+                }
                 *(f32x4*)(rowp + d0) = v;
             }
         }
@@ -483,7 +500,7 @@ __device__ void flash_bwd_dq(const AttnParams& p) {
         for (int d = 0; d < DB; d++)
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[d][r] = acc[d][r] + xch[(d * 16 + r) * 64 + lane];
-        att_store_rows<HD>(p.out + (rowbase + qpos) * p.ldq + qcol, acc, half, 1.0f);
+        att_store_rows<HD>(p.out + (rowbase + qpos) * p.ldq + qcol, acc, half, 1.0f, p.rope_cos, p.rope_sin, qpos);
     }
 }
 
@@ -632,7 +649,7 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
                 dvv[d][r] = dvv[d][r] + xch[(DB * 16 + d * 16 + r) * 64 + lane];
             }
         float* row = p.out + (rowbase + kpos) * p.ldq;
-        att_store_rows<HD>(row + kcol, dk, half, 1.0f);
+        att_store_rows<HD>(row + kcol, dk, half, 1.0f, p.rope_cos, p.rope_sin, kpos);
         att_store_rows<HD>(row + vcol, dvv, half, 1.0f);
     }
 }

@@ -10,7 +10,7 @@
 // Kernels:
 //   k_cache_fill        prefill: copy K, V of a [B*len, 3D] qkv into the cache
 //   k_decode_qkv_append step: RoPE the new q, k at position pos (same
-//                       arithmetic as k_rope_qk), append k, v to the cache
+//                       arithmetic as the QKV GEMM's RoPE epilogue), append k, v to the cache
 //   k_decode_attn_hd*   step: one (sequence, head, context chunk) per block;
 //                       writes the chunk's (max, sum, unnormalised O)
 //   k_decode_merge_hd*  step: combines the chunks in chunk order
@@ -44,7 +44,7 @@ k_cache_fill(const float* __restrict__ qkv, int ldq, int B, int len, int H, int 
 }
 
 // One thread per (sequence b, head h, pair k): rotate q and k of the new
-// token (row b of qkv) by position pos = *pos_dev exactly as k_rope_qk does,
+// token (row b of qkv) by position pos = *pos_dev as the QKV GEMM epilogue does,
 // write q back, append the rotated k and the v pair at cache position pos.
 // The position lives in device memory so that a captured step replays
 // unchanged (k_decode_advance moves it on).

@@ -49,7 +49,24 @@ struct GemmParams {
     int stats_ld;      // float2 entries per row of stats
     float* csum;       // optional (TB = 0): column sums of B over k (a bias gradient);
                        // with split-K each split writes its partial as row M of its slab
+    const float* rope_cos;   // optional: RoPE on columns [0, rope_cols) (see rope4)
+    const float* rope_sin;
+    int rope_T, rope_hd, rope_cols;
 };
+
+// RoPE of four consecutive output columns n..n+3 of row `row` (model/rope.c:
+// 20-40): pairs (2k, 2k+1) of a head of rope_hd columns rotated by
+// (cos, sin)[t = row % rope_T, k]; the tables are [rope_T][rope_hd/2].
+__device__ __forceinline__ void rope4(const GemmParams& p, int row, int n, f32x4& v) {
+    const int t = row % p.rope_T, k = (n % p.rope_hd) >> 1, hh = p.rope_hd >> 1;
+    const float c0 = p.rope_cos[t * hh + k], c1 = p.rope_cos[t * hh + k + 1];
+    const float s0 = p.rope_sin[t * hh + k], s1 = p.rope_sin[t * hh + k + 1];
+    const f32x4 a = v;
+    v[0] = a[0] * c0 - a[1] * s0;
+    v[1] = a[0] * s0 + a[1] * c0;
+    v[2] = a[2] * c1 - a[3] * s1;
+    v[3] = a[2] * s1 + a[3] * c1;
+}
 
 __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
     const int num = p.tiles_m * p.tiles_n;
@@ -419,7 +436,9 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                             if (p.resid) x = av[jj][g][q] + x;
                             v[q] = x;
                         }
-                        *(f32x4*)(crow + c0 + (j0 + jj) * 32 + 8 * g + 4 * half) = v;
+                        const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
+                        if (p.rope_cos && n < p.rope_cols) rope4(p, row, n, v);
+                        *(f32x4*)(crow + n) = v;
                     }
             }
         }
@@ -444,17 +463,20 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                     rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
                     bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
                 }
+                f32x4 v;
 #pragma unroll
                 for (int q = 0; q < 4; q++) {
-                    const int n = c0 + j * 32 + 8 * g + 4 * half + q;
-                    if (n < p.N) {
-                        float x = p.alpha * acc[i][j][4 * g + q];
-                        if (p.beta != 0.f) x = x + p.beta * cv[q];
-                        if (p.bias) x = x + bv[q];
-                        if (p.resid) x = rv[q] + x;
-                        crow[n] = x;
-                    }
+                    float x = p.alpha * acc[i][j][4 * g + q];
+                    if (p.beta != 0.f) x = x + p.beta * cv[q];
+                    if (p.bias) x = x + bv[q];
+                    if (p.resid) x = rv[q] + x;
+                    v[q] = x;
                 }
+                const int n0g = c0 + j * 32 + 8 * g + 4 * half;
+                if (p.rope_cos && n0g < p.rope_cols) rope4(p, row, n0g, v);
+#pragma unroll
+                for (int q = 0; q < 4; q++)
+                    if (n0g + q < p.N) crow[n0g + q] = v[q];
             }
     }
 }
@@ -547,7 +569,7 @@ GEMM_LAYOUTS(128x128, 128, 128, 16, 3)
 GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 2)
 GEMM_LAYOUTS(64x128, 64, 128, 16, 4)
 GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 2)
-GEMM_LAYOUTS(64x64, 64, 64, 16, 8)
+GEMM_LAYOUTS(64x64, 64, 64, 16, 5)
 GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 4)
 GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1)
 GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1)

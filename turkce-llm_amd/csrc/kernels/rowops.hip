@@ -230,43 +230,6 @@ k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __res
     }
 }
 
-// ---------------------------------------------------------------- RoPE
-// In place on the Q and K column ranges of qkv [N, ld]: pair (2k, 2k+1) of
-// head h at position t rotated by (cos, sin)[t, k] (rope.c:20-40); inverse
-// applies the transpose (model_ops.c:130-155).
-extern "C" __global__ void __launch_bounds__(256)
-k_rope_qk(float* __restrict__ qkv, const float* __restrict__ cos_t, const float* __restrict__ sin_t, int N, int T,
-          int H, int hd, int ld, int inverse) {
-    // one thread per (row n, head h, pair group k2): pairs 2*k2 and 2*k2+1,
-    // i.e. the float4 at columns h*hd + 4*k2 of the Q part and of the K part
-    const int half = hd >> 1, q4 = hd >> 2, D = H * hd;
-    long long total = (long long)N * H * q4;
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= total) return;
-    int k2 = (int)(i % q4);
-    long long rest = i / q4;
-    int h = (int)(rest % H);
-    long long n = rest / H;
-    int t = (int)(n % T);
-    const int k = 2 * k2;
-    const float c0 = cos_t[t * half + k], s0 = sin_t[t * half + k];
-    const float c1 = cos_t[t * half + k + 1], s1 = sin_t[t * half + k + 1];
-    float* row = qkv + n * (long long)ld + h * hd + 4 * k2;
-#pragma unroll
-    for (int part = 0; part < 2; part++) {
-        f32x4 a = *(f32x4*)(row + part * D);
-        f32x4 o;
-        if (!inverse) {
-            o[0] = a[0] * c0 - a[1] * s0; o[1] = a[0] * s0 + a[1] * c0;
-            o[2] = a[2] * c1 - a[3] * s1; o[3] = a[2] * s1 + a[3] * c1;
-        } else {
-            o[0] = a[0] * c0 + a[1] * s0; o[1] = -a[0] * s0 + a[1] * c0;
-            o[2] = a[2] * c1 + a[3] * s1; o[3] = -a[2] * s1 + a[3] * c1;
-        }
-        *(f32x4*)(row + part * D) = o;
-    }
-}
-
 // ---------------------------------------------------------------- SwiGLU
 // h = (g * sigmoid(g)) * u over gu = [gate | up] (feedforward.c:146-150).
 extern "C" __global__ void __launch_bounds__(256)

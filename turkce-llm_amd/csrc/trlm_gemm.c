@@ -39,6 +39,9 @@ typedef struct GemmParams {
     float* stats;
     int stats_ld;
     float* csum;
+    const float* rope_cos;
+    const float* rope_sin;
+    int rope_T, rope_hd, rope_cols;
 } GemmParams;
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
@@ -222,14 +225,20 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
                i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr) {
     trlm_gemm_ex(e, trans_a, trans_b, A, B, C, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta, bias, resid,
-                 ldr, 0, 0, 0);
+                 ldr, NULL);
 }
 
 i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
-                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr,
-                 hipDeviceptr_t stats, i32 stats_cap, hipDeviceptr_t csum) {
+                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x) {
+    hipDeviceptr_t stats = x ? x->stats : NULL, csum = x ? x->csum : NULL;
+    i32 stats_cap = x ? x->stats_cap : 0;
+    int rope = x && x->rope_cos;
     if (M <= 0 || N <= 0 || batch == 0) return 0;
+    if (rope && (batch != 1 || x->rope_T <= 0 || x->rope_hd <= 0 || x->rope_hd % 4 || x->rope_cols % 4)) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: RoPE epilogue needs a single GEMM and head width a multiple of 4\n");
+        _exit(1);
+    }
     if (stats && (batch != 1 || beta != 0.0f || bias || resid)) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single GEMM with no beta, bias or residual\n");
         _exit(1);
@@ -252,6 +261,10 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
     p.splits = 1; p.kchunk = K > 0 ? K : 1;
     p.alpha = alpha; p.beta = beta;
     p.csum = (float*)csum;
+    if (rope) {
+        p.rope_cos = x->rope_cos; p.rope_sin = x->rope_sin;
+        p.rope_T = x->rope_T; p.rope_hd = x->rope_hd; p.rope_cols = x->rope_cols;
+    }
 
     int layout = trans_a ? (trans_b ? 3 : L_TN) : (trans_b ? L_NT : L_NN);
     int aligned = layout != 3 && aligned16(A) && aligned16(B) && (lda % 4 == 0) && (ldb % 4 == 0) &&
@@ -272,7 +285,7 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
         splits = batch == 1 ? auto_splits(tiles_of(tile, M, N, 1), K) : 1;
     }
     if (e->force_splits > 0 && batch == 1) splits = e->force_splits;
-    if (stats) splits = 1;                 /* statistics need whole sums */
+    if (stats || rope) splits = 1;         /* these epilogues need whole sums */
     p.tiles_m = cdiv(M, TILES[tile].bm);
     p.tiles_n = cdiv(N, TILES[tile].bn);
     if (stats) set_stats(&p, stats, stats_cap, TILES[tile].bn);
