@@ -33,6 +33,8 @@
 //    contiguous, M-grouped range of tiles and reuses operands in its own L2.
 #include "common.h"
 
+#include <type_traits>
+
 struct GemmParams {
     const float* A;
     const float* B;
@@ -481,7 +483,95 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
     }
 }
 
-template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED>
+// As gemm_mainloop_full, with the global loads two tiles ahead: tile j >= 1
+// is staged in register set (j - 1) & 1, so the load of tile kt + 3 is
+// issued at the end of tile kt and has two tiles of MFMAs to land before
+// its LDS store at the end of tile kt + 2.  The k loop is unrolled by two so
+// that the register set and the LDS buffer are compile-time indices.
+template <int TA, int TB, int BM, int BN, int BK>
+__device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const float* A, const float* B, int m0,
+                                                  int n0, int kb, int ke, float* lds,
+                                                  f32x16 (&acc)[BM / 64][BN / 64], bool cs_on, f32x4& cs) {
+    constexpr bool AK = (TA == 0);
+    constexpr bool BK_ = (TB == 1);
+    constexpr int WM = BM / 2, WN = BN / 2;
+    constexpr int FM = WM / 32, FN = WN / 32;
+    constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
+    constexpr int NLA = BM * BK / 4 / 256, NLB = BN * BK / 4 / 256;
+    constexpr int NC = BK / 8;
+    static_assert(NC % 2 == 0, "fragment buffers alternate per 8-k chunk");
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int wm0 = (wave >> 1) * WM, wn0 = (wave & 1) * WN;
+
+    f32x4 ra[2][NLA], rb[2][NLB];
+    TileStream<BM, BK, AK> sa;
+    TileStream<BN, BK, BK_> sb;
+    sa.init(A, p.lda, m0, kb);
+    sb.init(B, p.ldb, n0, kb);
+    const int nk = (ke - kb) / BK;
+    sa.load(ra[0]);
+    sb.load(rb[0]);
+    store_tile<BM, BK, AK>(lds, ra[0]);
+    store_tile<BN, BK, BK_>(lds + ASZ, rb[0]);
+    if (!BK_ && cs_on) colsum_add<BN, BK, NLB>(cs, rb[0]);
+    if (nk > 1) {
+        sa.load(ra[0]);
+        sb.load(rb[0]);
+    }
+    if (nk > 2) {
+        sa.load(ra[1]);
+        sb.load(rb[1]);
+    }
+    __syncthreads();
+    f32x4 fa[2][FM], fb[2][FN];
+    fetch_frags<BM, BK, AK, FM>(lds, wm0, 0, lane, fa[0]);
+    fetch_frags<BN, BK, BK_, FN>(lds + ASZ, wn0, 0, lane, fb[0]);
+    // one tile: kt is computed from LDS buffer S = kt & 1; tile kt + 1 sits in
+    // register set S and goes to buffer S ^ 1; set S then takes tile kt + 3
+    auto tile = [&](auto S_, int kt) {
+        constexpr int S = decltype(S_)::value;
+        const float* la = lds + S * (ASZ + BSZ);
+        float* ln = lds + (S ^ 1) * (ASZ + BSZ);
+#pragma unroll
+        for (int c = 0; c < NC; c++) {
+            const int u = c & 1, v = u ^ 1;
+            if (c + 1 < NC) {
+                fetch_frags<BM, BK, AK, FM>(la, wm0, (c + 1) * 8, lane, fa[v]);
+                fetch_frags<BN, BK, BK_, FN>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
+            } else {
+                if (kt + 1 < nk) {
+                    store_tile<BM, BK, AK>(ln, ra[S]);
+                    store_tile<BN, BK, BK_>(ln + ASZ, rb[S]);
+                    if (!BK_ && cs_on) colsum_add<BN, BK, NLB>(cs, rb[S]);
+                }
+                __syncthreads();
+                if (kt + 1 < nk) {
+                    fetch_frags<BM, BK, AK, FM>(ln, wm0, 0, lane, fa[v]);
+                    fetch_frags<BN, BK, BK_, FN>(ln + ASZ, wn0, 0, lane, fb[v]);
+                    if (kt + 3 < nk) {
+                        sa.load(ra[S]);
+                        sb.load(rb[S]);
+                    }
+                }
+            }
+            __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+            for (int s = 0; s < 4; s++)
+#pragma unroll
+                for (int i = 0; i < FM; i++)
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+                        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u][j][s], fa[u][i][s], acc[i][j], 0, 0, 0);
+            __builtin_amdgcn_s_setprio(0);
+        }
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+        tile(std::integral_constant<int, 0>{}, kt);
+        if (kt + 1 < nk) tile(std::integral_constant<int, 1>{}, kt + 1);
+    }
+}
+
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED, int PF = 1>
 __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
@@ -520,7 +610,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     const bool cs_on = TB == 0 && p.csum != nullptr && tm == 0;
     f32x4 cs = {0.f, 0.f, 0.f, 0.f};
     if constexpr (ALIGNED) {
-        if (full) gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+        if (full) {
+            if constexpr (PF == 2) gemm_mainloop_pf2<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+            else gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+        }
         else gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
     } else {
         gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
@@ -546,35 +639,37 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
 }
 
-#define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE)                                 \
+#define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE, PF)                             \
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(WPE))) \
     NAME(GemmParams p) {                                                                 \
-        gemm_body<TA, TB, BM, BN, BK, AL>(p);                                            \
+        gemm_body<TA, TB, BM, BN, BK, AL, PF>(p);                                        \
     }
 
-#define GEMM_LAYOUTS(TILE, BM, BN, BK, WPE)                                             \
-    GEMM_KERNEL(k_gemm_nn_##TILE, 0, 0, BM, BN, BK, true, WPE)                          \
-    GEMM_KERNEL(k_gemm_nt_##TILE, 0, 1, BM, BN, BK, true, WPE)                          \
-    GEMM_KERNEL(k_gemm_tn_##TILE, 1, 0, BM, BN, BK, true, WPE)
+#define GEMM_LAYOUTS(TILE, BM, BN, BK, WPE, PF)                                         \
+    GEMM_KERNEL(k_gemm_nn_##TILE, 0, 0, BM, BN, BK, true, WPE, PF)                      \
+    GEMM_KERNEL(k_gemm_nt_##TILE, 0, 1, BM, BN, BK, true, WPE, PF)                      \
+    GEMM_KERNEL(k_gemm_tn_##TILE, 1, 0, BM, BN, BK, true, WPE, PF)
 
 // name: k_gemm_<layout>_<BM>x<BN>[_k32][_u]
 //   _k32: 32-deep k step (one barrier per 32 k instead of 16)
 //   _u:   unaligned operands (scalar loads), 16-deep k step
-// Waves own (BM/2)x(BN/2).  The last argument is the register budget as
-// resident waves per SIMD: the largest count the variant's LDS allows (2 for
-// the 8-accumulator-block 256x128 / 128x256 tiles), short of spilling.
-GEMM_LAYOUTS(256x128, 256, 128, 16, 2)
-GEMM_LAYOUTS(128x256, 128, 256, 16, 2)
-GEMM_LAYOUTS(128x128, 128, 128, 16, 3)
-GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 2)
-GEMM_LAYOUTS(64x128, 64, 128, 16, 4)
-GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 2)
-GEMM_LAYOUTS(64x64, 64, 64, 16, 5)
-GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 4)
-GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1)
-GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1)
-GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, 16, false, 1)
-GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, 16, false, 1)
+// Waves own (BM/2)x(BN/2).  WPE is the register budget as resident waves per
+// SIMD: the largest count the variant's LDS allows (2 for the
+// 8-accumulator-block 256x128 / 128x256 tiles), short of spilling.  PF is the
+// interior loop's global-load distance in tiles (2 where the second staging
+// register set fits the budget: 2-5 % faster on the model's shapes).
+GEMM_LAYOUTS(256x128, 256, 128, 16, 2, 1)
+GEMM_LAYOUTS(128x256, 128, 256, 16, 2, 1)
+GEMM_LAYOUTS(128x128, 128, 128, 16, 3, 2)
+GEMM_LAYOUTS(128x128_k32, 128, 128, 32, 2, 1)
+GEMM_LAYOUTS(64x128, 64, 128, 16, 4, 1)
+GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 2, 2)
+GEMM_LAYOUTS(64x64, 64, 64, 16, 5, 1)
+GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 4, 2)
+GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1, 1)
+GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1, 1)
+GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, 16, false, 1, 1)
+GEMM_KERNEL(k_gemm_tt_64x64_u, 1, 1, 64, 64, 16, false, 1, 1)
 
 // out[m,n] = alpha * sum_s W[s][m,n] (+ beta*out) (+ bias[n]); out = resid + v.
 // Partials are summed in split order, so the result is reproducible.
