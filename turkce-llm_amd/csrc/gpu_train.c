@@ -585,7 +585,7 @@ void trlm_train_step_queued(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay,
         hip_launch(g->k.sumsq_partial, GPU_TRAIN_NORM_BLOCKS, 1, 1, 256, 1, 1, 0, args);
         i32 np = (i32)GPU_TRAIN_NORM_BLOCKS;
         void* args2[] = { &part, &np, &clip, &norm_out, &scale_buf };
-        hip_launch(g->k.norm_clip, 1, 1, 1, 64, 1, 1, 0, args2);
+        hip_launch(g->k.norm_clip, 1, 1, 1, 256, 1, 1, 0, args2);
     }
     opt->t++;
     f32 bc1 = 1.0f - m_powf(opt->beta1, (f32)opt->t);
@@ -604,7 +604,7 @@ void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc) {
     hipDeviceptr_t rows = g->loss_rows;
     i32 B = (i32)g->B, T = (i32)g->T;
     void* args[] = { &rows, &B, &T, &out, &acc };
-    hip_launch(g->k.loss_mean, 1, 1, 1, 256, 1, 1, g->B * (u32)sizeof(f32), args);
+    hip_launch(g->k.loss_mean, 1, 1, 1, 256, 1, 1, 0, args);
 }
 
 /* eval_loss with the batch already on the device; the loss is added onto

@@ -416,12 +416,23 @@ k_argmax_rows(const float* __restrict__ logits, int ld, int V, unsigned* __restr
 // ---------------------------------------------------------------- grad norm
 // Per-block partial sums of squares over a fixed 1024x256 grid-stride layout
 // (train_kernels.cu:777-784); the host adds the partials in f64 in order.
+// Each thread's sum runs over its elements in index order; the loads of 16
+// consecutive strides are issued together ahead of their adds.
 extern "C" __global__ void __launch_bounds__(256)
 k_sumsq_partial(const float* __restrict__ x, long long n, float* __restrict__ partial) {
     __shared__ float ws[4];
+    constexpr int U = 16;
+    const long long stride = (long long)gridDim.x * blockDim.x;
+    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     float s = 0.f;
-    for (long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (long long)gridDim.x * blockDim.x)
-        s += x[i] * x[i];
+    for (; i + (U - 1) * stride < n; i += U * stride) {
+        float v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) v[u] = x[i + u * stride];
+#pragma unroll
+        for (int u = 0; u < U; u++) s += v[u] * v[u];
+    }
+    for (; i < n; i += stride) s += x[i] * x[i];
     s = wave_sum(s);
     if ((threadIdx.x & 63) == 0) ws[threadIdx.x >> 6] = s;
     __syncthreads();
@@ -491,23 +502,40 @@ k_adam_ds(float* __restrict__ p, const float* __restrict__ g, float* __restrict_
 // losses are added in order in f32 and divided by T, then the B means are
 // added in order and divided by B -- the host function's operation sequence.
 // acc != 0 adds the result onto *out (the validation sum over batches,
-// training/train_lm_gpu.c:241-253); otherwise it is stored.  Dynamic LDS:
-// B floats.
+// training/train_lm_gpu.c:241-253); otherwise it is stored.  One workgroup:
+// up to 256 sequences at a time, each summed by one thread from column
+// chunks that the whole workgroup stages in LDS with coalesced loads.
+#define LOSS_MEAN_CHUNK 4096
 extern "C" __global__ void __launch_bounds__(256)
 k_loss_mean(const float* __restrict__ rows, int B, int T, float* __restrict__ out, int acc) {
 #pragma clang fp contract(off)
-    extern __shared__ float seq_mean[];
-    for (int b = threadIdx.x; b < B; b += blockDim.x) {
-        const float* r = rows + (long long)b * T;
+    __shared__ float buf[LOSS_MEAN_CHUNK];
+    __shared__ float means[256];
+    float total = 0.f;   // thread 0: the in-order sum of the sequence means
+    for (int b0 = 0; b0 < B; b0 += 256) {
+        const int nb = B - b0 < 256 ? B - b0 : 256;
+        const int tc = LOSS_MEAN_CHUNK / nb;
         float s = 0.f;
-        for (int t = 0; t < T; t++) s += r[t];
-        seq_mean[b] = s / (float)T;
+        for (int t0 = 0; t0 < T; t0 += tc) {
+            const int w = T - t0 < tc ? T - t0 : tc;
+            __syncthreads();
+            for (int e = threadIdx.x; e < nb * w; e += 256) {
+                const int r = e / w, c = e - r * w;
+                buf[e] = rows[(long long)(b0 + r) * T + t0 + c];
+            }
+            __syncthreads();
+            if ((int)threadIdx.x < nb) {
+                const float* q = buf + threadIdx.x * w;
+                for (int c = 0; c < w; c++) s += q[c];
+            }
+        }
+        if ((int)threadIdx.x < nb) means[threadIdx.x] = s / (float)T;
+        __syncthreads();
+        if (threadIdx.x == 0)
+            for (int b = 0; b < nb; b++) total += means[b];
     }
-    __syncthreads();
     if (threadIdx.x == 0) {
-        float sum = 0.f;
-        for (int b = 0; b < B; b++) sum += seq_mean[b];
-        const float mean = sum / (float)B;
+        const float mean = total / (float)B;
         *out = (acc ? *out : 0.0f) + mean;
     }
 }
@@ -536,13 +564,24 @@ __device__ double ref_sqrt64(double x) {
 // Grad norm (model/gpu_train.c:502-512: the fixed-grid partial sums added in
 // block order in f64, then m_sqrt) and the driver's clip scale
 // (training/train_lm_gpu.c:218-220: clip/norm in f64, rounded to f32, when
-// the norm exceeds clip; 1 otherwise; clip <= 0 never clips).  One thread.
-extern "C" __global__ void k_norm_clip(const float* __restrict__ partial, int n, double clip,
-                                       double* __restrict__ norm_out, float* __restrict__ scale_out) {
+// the norm exceeds clip; 1 otherwise; clip <= 0 never clips).  The
+// workgroup stages the partials in LDS; thread 0 adds them in order.
+#define NORM_CLIP_CHUNK 4096
+extern "C" __global__ void __launch_bounds__(256) k_norm_clip(const float* __restrict__ partial, int n, double clip,
+                                                             double* __restrict__ norm_out,
+                                                             float* __restrict__ scale_out) {
 #pragma clang fp contract(off)
-    if (threadIdx.x != 0) return;
+    __shared__ float buf[NORM_CLIP_CHUNK];
     double ss = 0.0;
-    for (int i = 0; i < n; i++) ss += (double)partial[i];
+    for (int i0 = 0; i0 < n; i0 += NORM_CLIP_CHUNK) {
+        const int w = n - i0 < NORM_CLIP_CHUNK ? n - i0 : NORM_CLIP_CHUNK;
+        __syncthreads();
+        for (int e = threadIdx.x; e < w; e += blockDim.x) buf[e] = partial[i0 + e];
+        __syncthreads();
+        if (threadIdx.x == 0)
+            for (int e = 0; e < w; e++) ss += (double)buf[e];
+    }
+    if (threadIdx.x != 0) return;
     const double nrm = ref_sqrt64(ss);
     *norm_out = nrm;
     *scale_out = (clip > 0.0 && nrm > clip) ? (float)(clip / nrm) : 1.0f;

@@ -24,7 +24,6 @@
 
 #define LR_PI 3.14159265358979323846
 #define SLOTS 3          /* pinned batch buffers in flight */
-#define LOSS_MEAN_MAX_B 16384u   /* k_loss_mean keeps B floats in LDS */
 
 static void loop_fatal(const char* what) {
     fprintf(stderr, "[HIP ERROR] train_loop: %s\n", what);
@@ -103,7 +102,6 @@ void gpu_trainer_train_steps(GpuTrainer* g, AdamOptimizer* opt, const u32* token
     trlm_bind(g);
     if (n_steps == 0) return;
     if (num_tokens < (u64)g->T + 2) loop_fatal("token stream shorter than seq_len + 2");
-    if (g->B > LOSS_MEAN_MAX_B) loop_fatal("batch too large for the device loss mean");
     u32 N = g->N;
     Ring ring;
     ring_open(&ring, N);
@@ -142,7 +140,6 @@ void gpu_trainer_train_steps(GpuTrainer* g, AdamOptimizer* opt, const u32* token
 f32 gpu_trainer_eval_windows(GpuTrainer* g, const u32* tokens, u64 train_tokens, u64 val_tokens, u32 val_batches) {
     trlm_bind(g);
     if (val_batches == 0) loop_fatal("val_batches is 0");
-    if (g->B > LOSS_MEAN_MAX_B) loop_fatal("batch too large for the device loss mean");
     u64 windows = (u64)val_batches * g->B;
     if (val_tokens < (u64)g->T + 1) loop_fatal("validation block shorter than seq_len + 1");
     u64 stride = (val_tokens - g->T - 1) / windows;
