@@ -43,7 +43,7 @@ typedef struct TrlmGemm TrlmGemm;
 typedef struct GpuKernels {
     hipFunction_t fill_zero, embed_fwd, embed_bwd, rmsnorm_fwd, rmsnorm_bwd, colsum_final;
     hipFunction_t swiglu_fwd, swiglu_bwd, cross_entropy, argmax_rows, sumsq_partial, adam;
-    hipFunction_t attn_fwd, attn_bwd_dkv, attn_bwd_dq;
+    hipFunction_t attn_fwd, attn_bwd_dkv, attn_bwd_dq, attn_dvec;
     hipFunction_t loss_mean, norm_clip, adam_ds;   /* queued driver steps (trlm_ext.h) */
 } GpuKernels;
 
@@ -66,6 +66,7 @@ typedef struct GpuTrainer {
     hipDeviceptr_t x_final, nf, rf, logits;   /* logits [N, ldv]: gradient after the CE */
 
     hipDeviceptr_t dres, dn, datt, dqkv, dh, dgu, dvec, part;
+    hipDeviceptr_t att_ds;                    /* attention backward: causal dS blocks of one layer */
 
     hipDeviceptr_t ids, targets, loss_rows, cos_t, sin_t;
     hipDeviceptr_t emb_order, emb_seg;        /* embedding-backward row groups */

@@ -110,6 +110,7 @@ def test_code_object_has_every_kernel(trlm):
         src += open(os.path.join(ROOT, "turkce-llm_amd", "csrc", f)).read()
     names = set(re.findall(r'"(k_[a-z0-9_]+)"', src))
     names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_attn_dvec_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_decode_attn_hd%d" % d for d in (16, 32, 64)} | {"k_decode_merge_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in (

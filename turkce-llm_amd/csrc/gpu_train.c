@@ -117,6 +117,7 @@ typedef struct AttnParams {
     float scale;
     const float* rope_cos;
     const float* rope_sin;
+    float* ds;
 } AttnParams;
 
 static AttnParams attn_params(GpuTrainer* g) {
@@ -194,6 +195,10 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.dh = dalloc(N * F);
     g.dgu = dalloc(N * 2 * F);
     g.dvec = dalloc(BHT);
+    {
+        u64 nqb = ((u64)g.T + 63) / 64;
+        g.att_ds = dalloc((u64)g.B * g.H * (nqb * (nqb + 1) / 2) * 4096);
+    }
     u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;   /* RMSNorm weight-gradient partials */
     g.part = dalloc(part_rows * D);
 
@@ -241,6 +246,8 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.attn_bwd_dkv = hip_get_kernel(c, name);
     snprintf(name, sizeof(name), "k_attn_bwd_dq_hd%u", g.hd);
     g.k.attn_bwd_dq = hip_get_kernel(c, name);
+    snprintf(name, sizeof(name), "k_attn_dvec_hd%u", g.hd);
+    g.k.attn_dvec = hip_get_kernel(c, name);
 
     gpu_trainer_upload(&g, params, NULL_PTR);
     hip_sync();
@@ -478,10 +485,13 @@ static void backward_pass(GpuTrainer* g) {
         gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
         ap.qkv = (const float*)a->qkv; ap.O = (const float*)a->att; ap.dO = (const float*)g->datt;
         ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
+        ap.ds = (float*)g->att_ds;
         {
+            /* D, then dK/dV (leaving dS), then dQ from dS */
             void* args[] = { &ap };
-            hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_dvec, cdiv_u64((u64)g->N * g->D / 4, 256), 1, 1, 256, 1, 1, 0, args);
             hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
+            hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
         gemm_wb(g, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
         gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,

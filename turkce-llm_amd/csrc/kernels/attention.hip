@@ -5,8 +5,10 @@
 // gpu_train.c:346-353,445-455) with kernels that never store P:
 //   forward : S = QK^T*scale, online softmax, O = PV; saves the per-row
 //             log-sum-exp (base 2) for the backward;
-//   backward: dQ over query blocks (also writing D_i = <dO_i, O_i>), then
-//             dK, dV over key blocks.
+//   backward: D_i = <dO_i, O_i>; dK, dV over key blocks, which also store
+//             every causal 64x64 block of dS = P o (dP - D) * scale; then
+//             dQ = dS K over query blocks from those blocks (S and dP are
+//             formed once, not once per pass).
 // Masked entries (j > i) are exactly zero in the reference (exp of -1e9 is 0,
 // mathlib.c:142), so key blocks above the diagonal are skipped outright.
 // No atomics: dQ is produced by its own pass instead of being accumulated
@@ -49,7 +51,19 @@ struct AttnParams {
     // projection
     const float* rope_cos;
     const float* rope_sin;
+    // backward: the dK/dV pass leaves every causal 64x64 block of
+    // dS = P o (dP - D) * scale here for the dQ pass: [B*H][nqb(nqb+1)/2]
+    // blocks (query block i, key block j <= i at i(i+1)/2 + j), each in the
+    // dK/dV pass's register order [key group g][query half c][r][lane]: key
+    // 32g + l%32, query 32c + 8(r/4) + 4(l/32) + r%4 (one 256-byte row per r)
+    float* ds;
 };
+
+// First float of dS block (query block qb, key block kb <= qb) of head bh.
+__device__ __forceinline__ float* att_ds_block(const AttnParams& p, int bh, int qb, int kb) {
+    const long long nqb = (p.T + 63) / 64;
+    return p.ds + (((long long)bh * (nqb * (nqb + 1) / 2)) + (long long)qb * (qb + 1) / 2 + kb) * 4096;
+}
 
 // One [64 x HD] tile (rows r0.., columns col0.., row stride ld) held in
 // registers across the 256 threads of a workgroup: thread t holds the
@@ -373,137 +387,6 @@ __device__ void flash_fwd(const AttnParams& p) {
     }
 }
 
-// =========================================================== backward dQ
-// grid (B*H, ceil(T/64)).  Same split as the forward: query group x key
-// partition; S^T and dP^T put one query per lane; dQ^T += K^T dS^T.  Also
-// writes D_i = <dO_i, O_i> for the dK/dV pass.
-template <int HD>
-__device__ void flash_bwd_dq(const AttnParams& p) {
-    constexpr int DB = (HD + 31) / 32;
-    constexpr int LD = HD + 4;
-    __shared__ __attribute__((aligned(16))) float lds[4 * 64 * LD];
-
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
-    const int grp = wave & 1, part = wave >> 1;
-    const int nqb = (p.T + 63) / 64;
-    const int qb = nqb - 1 - (int)blockIdx.y;     // longest blocks first, as in the forward
-    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
-    const long long rowbase = (long long)b * p.T;
-    const float* qkv = p.qkv + rowbase * p.ldq;
-    const float* dO = p.dO + rowbase * p.ldo;
-    const int qcol = h * HD, kcol = p.D + h * HD, vcol = 2 * p.D + h * HD;
-    const float c2 = p.scale * ATT_LOG2E;
-    const int qw0 = qb * 64 + grp * 32;
-    const int qpos = qw0 + (lane & 31);
-    const bool qvalid = qpos < p.T;
-
-    f32x4 qf[HD / 8], gf[HD / 8];
-    att_frag_global<HD>(qkv, p.ldq, qpos, qvalid, qcol, lane, qf);
-    att_frag_global<HD>(dO, p.ldo, qpos, qvalid, qcol, lane, gf);
-    const float lq = qvalid ? p.lse[(long long)bh * p.T + qpos] : 0.f;
-    float dq_i;
-    {
-        f32x4 of[HD / 8];
-        att_frag_global<HD>(p.O + rowbase * p.ldo, p.ldo, qpos, qvalid, qcol, lane, of);
-        float pt = 0.f;
-#pragma unroll
-        for (int j = 0; j < HD / 8; j++)
-#pragma unroll
-            for (int t = 0; t < 4; t++) pt += gf[j][t] * of[j][t];
-        dq_i = pt + __shfl_xor(pt, 32, WAVE);
-        if (qvalid && half == 0 && part == 0) p.dvec[(long long)bh * p.T + qpos] = dq_i;
-    }
-
-    f32x16 acc[DB];
-#pragma unroll
-    for (int d = 0; d < DB; d++)
-#pragma unroll
-        for (int r = 0; r < 16; r++) acc[d][r] = 0.f;
-
-    int kv_end = (qb + 1) * 64;
-    if (kv_end > p.T) kv_end = p.T;
-    const int nkv = (kv_end + 63) / 64;
-    const int niter = (nkv + 1) / 2;
-    const float* Ks = lds + part * 2 * 64 * LD;
-    const float* Vs = Ks + 64 * LD;
-    for (int it = 0; it < niter; it++) {
-        // K, V of each of the stage's two key blocks: all loads of a block
-        // are in flight together, then stored (registers are too scarce
-        // here to fetch a whole stage ahead).  Unconditional, as in the
-        // forward: blocks past the end load clamped rows and store zeros.
-#pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            const int kbp = 2 * it + pp;
-            AttTile<HD> tk, tv;
-            tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
-            tv.load(qkv, p.ldq, kbp * 64, p.T, vcol);
-            if (pp == 0) __syncthreads();
-            tk.store(lds + pp * 2 * 64 * LD, kbp * 64, kv_end);
-            tv.store(lds + pp * 2 * 64 * LD + 64 * LD, kbp * 64, kv_end);
-        }
-        __syncthreads();
-        const int kb = 2 * it + part;
-        const int kv0 = kb * 64;
-        if (kb >= nkv || kv0 > qw0 + 31) continue;
-#pragma unroll
-        for (int c = 0; c < 2; c++) {
-            f32x16 s, dp;
-#pragma unroll
-            for (int r = 0; r < 16; r++) { s[r] = 0.f; dp[r] = 0.f; }
-#pragma unroll
-            for (int j = 0; j < HD / 8; j++) {
-                f32x4 ka = att_frag<HD>(Ks, c * 32, j, lane);
-                f32x4 va = att_frag<HD>(Vs, c * 32, j, lane);
-#pragma unroll
-                for (int t = 0; t < 4; t++) {
-                    s = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], qf[j][t], s, 0, 0, 0);
-                    dp = __builtin_amdgcn_mfma_f32_32x32x2f32(va[t], gf[j][t], dp, 0, 0, 0);
-                }
-            }
-            // P recomputed from the saved log-sum-exp; the causal mask only on
-            // the diagonal block (wave-uniform test)
-            f32x16 pr;
-#pragma unroll
-            for (int r = 0; r < 16; r++) pr[r] = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -lq));
-            if (kv0 + 63 > qw0) {
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (kpos > qpos) pr[r] = 0.f;
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < 16; r++) dp[r] = pr[r] * (dp[r] - dq_i) * p.scale;
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                const int kr = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-#pragma unroll
-                for (int d = 0; d < DB; d++) {
-                    const int dc = d * 32 + (lane & 31);
-                    float ka = (dc < HD) ? Ks[kr * LD + dc] : 0.f;
-                    acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka, dp[r], acc[d], 0, 0, 0);
-                }
-            }
-        }
-    }
-    __syncthreads();
-    float* xch = lds + grp * (DB * 16 * 64);
-    if (part == 1) {
-#pragma unroll
-        for (int d = 0; d < DB; d++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) xch[(d * 16 + r) * 64 + lane] = acc[d][r];
-    }
-    __syncthreads();
-    if (part == 0 && qvalid) {
-#pragma unroll
-        for (int d = 0; d < DB; d++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) acc[d][r] = acc[d][r] + xch[(d * 16 + r) * 64 + lane];
-        att_store_rows<HD>(p.out + (rowbase + qpos) * p.ldq + qcol, acc, half, 1.0f, p.rope_cos, p.rope_sin, qpos);
-    }
-}
-
 // =========================================================== backward dK, dV
 // grid (B*H, ceil(T/64)).  Wave w: key group g = w&1 (32 keys), query
 // partition part = w>>1 (64-query blocks at or after the keys' block,
@@ -516,7 +399,8 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     constexpr int TILE = 2 * 64 * LD + 128;                 // Q, dO, L, D of one query block
     __shared__ __attribute__((aligned(16))) float lds[2 * TILE];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform, kept in SGPRs
     const int grp = wave & 1, part = wave >> 1;
     const int kb = blockIdx.y;                               // early keys (most queries) first
     const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
@@ -614,6 +498,13 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
                 const int ql = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
                 dp[r] = s[r] * (dp[r] - Ds[ql]) * p.scale;
             }
+            {
+                // the registers as they are: 64 lanes = one 256-byte row per r
+                // (wave-uniform block base: scalar address, lane as the offset)
+                float* blk = att_ds_block(p, bh, kb + j, kb) + (grp * 2 + c) * 1024;
+#pragma unroll
+                for (int r = 0; r < 16; r++) blk[r * 64 + lane] = dp[r];
+            }
 #pragma unroll
             for (int r = 0; r < 16; r++) {
                 const int ql = c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
@@ -654,6 +545,117 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     }
 }
 
+// =========================================================== backward dQ
+// dQ_i = sum_{j <= i} dS_ij K_j from the dS blocks of the dK/dV pass.
+// grid (B*H, ceil(T/64)), 256 threads, longest query blocks first.  Wave w:
+// query group g = w&1 (32 queries), key partition part = w>>1 (key blocks
+// part, part+2, ...).  dQ^T accumulates as K^T dS^T: lane l feeds
+// K[k][d0 + l%32] and dS[q + l%32][k] for k = 8c + 4(l/32) + s, so the dS
+// operand of four k-steps is one 128-bit load (four consecutive keys are
+// four consecutive lanes of the stored register rows).
+template <int HD>
+__device__ void flash_bwd_dq_ds(const AttnParams& p) {
+    constexpr int DB = (HD + 31) / 32;
+    __shared__ __attribute__((aligned(16))) float lds[2 * HD * ATT_LDT];
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
+    const int grp = wave & 1, part = wave >> 1;
+    const int nqb = (p.T + 63) / 64;
+    const int qb = nqb - 1 - (int)blockIdx.y;
+    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
+    const long long rowbase = (long long)b * p.T;
+    const float* qkv = p.qkv + rowbase * p.ldq;
+    const int qcol = h * HD, kcol = p.D + h * HD;
+    const int qpos = qb * 64 + grp * 32 + (lane & 31);
+
+    f32x16 acc[DB];
+#pragma unroll
+    for (int d = 0; d < DB; d++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[d][r] = 0.f;
+
+    const int nkv = qb + 1;
+    const int niter = (nkv + 1) / 2;
+    const float* KT = lds + part * HD * ATT_LDT;
+    for (int it = 0; it < niter; it++) {
+        // K of the stage's two key blocks, transposed ([HD][ATT_LDT]); rows
+        // past the end are stored as zeros
+#pragma unroll
+        for (int pp = 0; pp < 2; pp++) {
+            const int kbp = 2 * it + pp;
+            AttTileT<HD> tk;
+            tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
+            if (pp == 0) __syncthreads();
+            tk.store(lds + pp * HD * ATT_LDT, kbp * 64, p.T);
+        }
+        __syncthreads();
+        const int kb = 2 * it + part;
+        if (kb >= nkv) continue;
+        // this lane's query qq = l%32 of group grp sits in rows r(qq) of the
+        // (key group, grp) sub-blocks, in lane half (qq/4)&1
+        const int qq = lane & 31;
+        const float* row = att_ds_block(p, bh, qb, kb) + grp * 1024 + ((qq >> 3) * 4 + (qq & 3)) * 64 +
+                           ((qq >> 2) & 1) * 32 + 4 * half;
+        f32x4 sv[8];
+#pragma unroll
+        for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
+#pragma unroll
+        for (int c = 0; c < 8; c++) {
+#pragma unroll
+            for (int d = 0; d < DB; d++) {
+                const int dc = d * 32 + (lane & 31);
+                const f32x4 ka = dc < HD ? *(const f32x4*)(KT + dc * ATT_LDT + 8 * c + 4 * half)
+                                         : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; t++) acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], sv[c][t], acc[d], 0, 0, 0);
+            }
+        }
+    }
+    __syncthreads();
+    float* xch = lds + grp * (DB * 16 * 64);
+    if (part == 1) {
+#pragma unroll
+        for (int d = 0; d < DB; d++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) xch[(d * 16 + r) * 64 + lane] = acc[d][r];
+    }
+    __syncthreads();
+    if (part == 0 && qpos < p.T) {
+#pragma unroll
+        for (int d = 0; d < DB; d++)
+#pragma unroll
+            for (int r = 0; r < 16; r++) acc[d][r] = acc[d][r] + xch[(d * 16 + r) * 64 + lane];
+        att_store_rows<HD>(p.out + (rowbase + qpos) * p.ldq + qcol, acc, half, 1.0f, p.rope_cos, p.rope_sin, qpos);
+    }
+}
+
+// D_i = <dO_i, O_i> per (row, head) for the dK/dV pass: HD/4 threads per
+// (row, head), one float4 product each, summed across them by shuffles.
+template <int HD>
+__device__ void attn_dvec(const AttnParams& p) {
+    constexpr int G = HD / 4;
+    const long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    const long long total = (long long)p.B * p.T * p.D / 4;
+    float v = 0.f;
+    long long rh = 0;
+    if (i < total) {
+        rh = i / G;                                       // row * H + h
+        const long long row = rh / p.H;
+        const int h = (int)(rh - row * p.H), c = (int)(i % G) * 4;
+        const f32x4 g = *(const f32x4*)(p.dO + row * p.ldo + h * HD + c);
+        const f32x4 o = *(const f32x4*)(p.O + row * p.ldo + h * HD + c);
+        v = g[0] * o[0] + g[1] * o[1] + g[2] * o[2] + g[3] * o[3];
+    }
+#pragma unroll
+    for (int m = G / 2; m > 0; m >>= 1) v += __shfl_xor(v, m, WAVE);
+    if (i < total && i % G == 0) {
+        const long long row = rh / p.H;
+        const int h = (int)(rh - row * p.H);
+        const long long bb = row / p.T, t = row - bb * p.T;
+        p.dvec[(bb * p.H + h) * p.T + t] = v;
+    }
+}
+
 #define ATT_KERNELS(HD)                                                                                   \
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_fwd_hd##HD(AttnParams p) { \
         flash_fwd<HD>(p);                                                                                 \
@@ -661,9 +663,10 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dkv_hd##HD(AttnParams p) { \
         flash_bwd_dkv<HD>(p);                                                                             \
     }                                                                                                     \
-    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dq_hd##HD(AttnParams p) { \
-        flash_bwd_dq<HD>(p);                                                                              \
-    }
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) k_attn_bwd_dq_hd##HD(AttnParams p) { \
+        flash_bwd_dq_ds<HD>(p);                                                                           \
+    }                                                                                                     \
+    extern "C" __global__ void __launch_bounds__(256) k_attn_dvec_hd##HD(AttnParams p) { attn_dvec<HD>(p); }
 
 ATT_KERNELS(16)
 ATT_KERNELS(32)
