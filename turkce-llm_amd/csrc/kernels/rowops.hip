@@ -525,8 +525,17 @@ k_loss_mean(const float* __restrict__ rows, int B, int T, float* __restrict__ ou
             }
             __syncthreads();
             if ((int)threadIdx.x < nb) {
+                // in order; 16 LDS reads in flight ahead of their adds
                 const float* q = buf + threadIdx.x * w;
-                for (int c = 0; c < w; c++) s += q[c];
+                int c = 0;
+                for (; c + 16 <= w; c += 16) {
+                    float v[16];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) v[u] = q[c + u];
+#pragma unroll
+                    for (int u = 0; u < 16; u++) s += v[u];
+                }
+                for (; c < w; c++) s += q[c];
             }
         }
         if ((int)threadIdx.x < nb) means[threadIdx.x] = s / (float)T;
@@ -578,8 +587,17 @@ extern "C" __global__ void __launch_bounds__(256) k_norm_clip(const float* __res
         __syncthreads();
         for (int e = threadIdx.x; e < w; e += blockDim.x) buf[e] = partial[i0 + e];
         __syncthreads();
-        if (threadIdx.x == 0)
-            for (int e = 0; e < w; e++) ss += (double)buf[e];
+        if (threadIdx.x == 0) {
+            int e = 0;
+            for (; e + 16 <= w; e += 16) {
+                float v[16];
+#pragma unroll
+                for (int u = 0; u < 16; u++) v[u] = buf[e + u];
+#pragma unroll
+                for (int u = 0; u < 16; u++) ss += (double)v[u];
+            }
+            for (; e < w; e++) ss += (double)buf[e];
+        }
     }
     if (threadIdx.x != 0) return;
     const double nrm = ref_sqrt64(ss);
