@@ -24,6 +24,8 @@ CASES = {
     "small_offgrid": dict(V=50, D=32, H=2, L=2, F=48, T=12, B=5, ntok=4000),
     "long_context": dict(V=500, D=64, H=2, L=2, F=128, T=1024, B=2, ntok=20000),
     "real_scale": dict(V=31769, D=384, H=6, L=12, F=1024, T=128, B=4, ntok=200000),
+    # several 64-row attention blocks with a ragged last one (hd 16)
+    "ragged_blocks": dict(V=300, D=64, H=4, L=2, F=96, T=200, B=3, ntok=8000),
 }
 TOL = 1e-4
 
