@@ -112,6 +112,42 @@ def test_gemm_offgrid(dev, M, N, K, ta, tb):
     assert ok, (var, rel)
 
 
+RAGGED_ALIGNED = [  # M, N, K: odd sizes, leading dims rounded up to 4
+    (301, 203, 605), (130, 70, 5001), (257, 129, 47), (8, 1031, 333),
+]
+
+
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+@pytest.mark.parametrize("M,N,K", RAGGED_ALIGNED)
+def test_gemm_ragged_aligned_nan_padding(dev, M, N, K, ta, tb):
+    """Edge tiles of the aligned kernels run the unchecked loop with their
+    out-of-range rows/columns redirected, and a partial last k step runs
+    guarded.  The stored rows are padded to a multiple of 4 with NaN: any
+    padding element that reached a stored output would show."""
+    rng = np.random.default_rng(M + 3 * N + 7 * K + ta + 2 * tb)
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+
+    def padded(x):
+        w = (x.shape[1] + 3) // 4 * 4
+        out = np.full((x.shape[0], w), np.nan, np.float32)
+        out[:, :x.shape[1]] = x
+        return out
+
+    As, Bs = padded(stored(A, ta)), padded(stored(B, tb))
+    dA, dB = dev.upload(As), dev.upload(Bs)
+    dC = dev.upload(np.zeros((M, N), np.float32))
+    dev.matmul(ta, tb, dA, dB, dC, M, N, K, As.shape[1], Bs.shape[1], N)
+    got = dev.download(dC, (M, N))
+    var = dev.last_variant()
+    for x in (dA, dB, dC):
+        dev.free(x)
+    assert "_u" not in var[0], var          # the aligned kernels ran
+    assert np.isfinite(got).all(), var
+    ok, rel = close(got, ref64(A, B))
+    assert ok, (var, rel)
+
+
 def test_gemm_small_integers_exact(dev):
     """test_cuda.c:55-94's case (4x3 @ 3x5 of small exact values): exact."""
     A = np.array([(i % 7) - 3.0 for i in range(12)], np.float32).reshape(4, 3)

@@ -167,14 +167,19 @@ __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, in
     }
 }
 
-// Interior-tile loads: every element of the R x BK tile is in bounds, so
-// each thread streams f32x4s through fixed row pointers with no checks.
+// Unchecked loads over whole BK steps: each thread streams f32x4s through
+// fixed row pointers.  The k-range must lie inside the matrix; rows (KMAJOR)
+// or columns (m/n-contiguous) past rlim are redirected to row rlim - 1 /
+// column 0, so an edge tile reads only valid memory and its extra rows /
+// columns hold copies that only reach the C rows / columns the epilogue
+// does not store.  (A float4 that straddles rlim stays inside the row: the
+// aligned kernels require ld % 4 == 0, so ld >= rlim rounded up to 4.)
 template <int R, int BK, bool KMAJOR>
 struct TileStream {
     static constexpr int NL = R * BK / 4 / 256;
     const float* ptr[NL];
     long long step;
-    __device__ __forceinline__ void init(const float* __restrict__ base, int ld, int r0, int k0) {
+    __device__ __forceinline__ void init(const float* __restrict__ base, int ld, int r0, int rlim, int k0) {
         const int t = threadIdx.x;
 #pragma unroll
         for (int i = 0; i < NL; i++) {
@@ -182,7 +187,9 @@ struct TileStream {
             int r, k;
             if (KMAJOR) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
             else { k = idx / (R / 4); r = (idx % (R / 4)) * 4; }
-            ptr[i] = KMAJOR ? base + (long long)(r0 + r) * ld + (k0 + k) : base + (long long)(k0 + k) * ld + (r0 + r);
+            int gr = r0 + r;
+            if (gr >= rlim) gr = KMAJOR ? rlim - 1 : 0;
+            ptr[i] = KMAJOR ? base + (long long)gr * ld + (k0 + k) : base + (long long)(k0 + k) * ld + gr;
         }
         step = KMAJOR ? BK : (long long)BK * ld;
     }
@@ -287,8 +294,8 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
     f32x4 ra[NLA], rb[NLB];
     TileStream<BM, BK, AK> sa;
     TileStream<BN, BK, BK_> sb;
-    sa.init(A, p.lda, m0, kb);
-    sb.init(B, p.ldb, n0, kb);
+    sa.init(A, p.lda, m0, p.M, kb);
+    sb.init(B, p.ldb, n0, p.N, kb);
     const int nk = (ke - kb) / BK;
     sa.load(ra);
     sb.load(rb);
@@ -506,8 +513,8 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
     f32x4 ra[2][NLA], rb[2][NLB];
     TileStream<BM, BK, AK> sa;
     TileStream<BN, BK, BK_> sb;
-    sa.init(A, p.lda, m0, kb);
-    sb.init(B, p.ldb, n0, kb);
+    sa.init(A, p.lda, m0, p.M, kb);
+    sb.init(B, p.ldb, n0, p.N, kb);
     const int nk = (ke - kb) / BK;
     sa.load(ra[0]);
     sb.load(rb[0]);
@@ -603,18 +610,23 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
 #pragma unroll
             for (int r = 0; r < 16; r++) acc[i][j][r] = 0.f;
 
-    // Interior tiles whose k-range is whole BK steps take the pipelined,
-    // check-free loop; edge tiles (and the scalar-load variants) the guarded one.
-    const bool full = ALIGNED && m0 + BM <= p.M && n0 + BN <= p.N && ke > kb && (ke - kb) % BK == 0;
+    // The whole BK steps of the k-range take the pipelined, check-free loop
+    // (edge tiles included: their out-of-range rows / columns are redirected,
+    // see TileStream); a partial last step, and the scalar-load variants,
+    // take the guarded loop.
+    const int kfull = ke > kb ? kb + (ke - kb) / BK * BK : kb;
     // the first row of tiles also sums B's columns over its k-range
     const bool cs_on = TB == 0 && p.csum != nullptr && tm == 0;
     f32x4 cs = {0.f, 0.f, 0.f, 0.f};
     if constexpr (ALIGNED) {
-        if (full) {
-            if constexpr (PF == 2) gemm_mainloop_pf2<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
-            else gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+        if (kfull > kb) {
+            if constexpr (PF == 2) gemm_mainloop_pf2<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, kfull, lds, acc, cs_on, cs);
+            else gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, kfull, lds, acc, cs_on, cs);
         }
-        else gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
+        if (kfull < ke) {
+            if (kfull > kb) __syncthreads();   // every wave is done reading the loop's LDS tiles
+            gemm_mainloop<TA, TB, BM, BN, BK, true>(p, A, B, m0, n0, kfull, ke, lds, acc, cs_on, cs);
+        }
     } else {
         gemm_mainloop<TA, TB, BM, BN, BK, false>(p, A, B, m0, n0, kb, ke, lds, acc, cs_on, cs);
     }
