@@ -158,19 +158,19 @@ static int auto_splits(long long tiles, int K) {
  * imbalance term proportional to a workgroup's duration.  Split-K adds the
  * partials' round trip through HBM plus the reduction launch.  Constants
  * fitted to MI355X timings of every variant/split on the model's GEMMs at
- * 512-8192 rows (within 0.8 % of the per-shape best over those 45 shapes). */
+ * 512-8192 rows (within 0.6 % of the per-shape best over those 45 shapes). */
 typedef struct PlanTile { int tile; int occ; double eff; } PlanTile;
 static const PlanTile PLAN_TILES[] = {
-    { T_128x128, 3, 1.105 }, { T_128x256, 2, 1.036 }, { T_256x128, 2, 1.09 },
-    { T_64x128_K32, 2, 1.03 }, { T_64x64_K32, 4, 1.067 },
+    { T_128x128, 3, 1.047 }, { T_128x256, 2, 0.977 }, { T_256x128, 2, 1.008 },
+    { T_64x128_K32, 2, 0.955 }, { T_64x64_K32, 4, 0.992 },
 };
 static const int PLAN_SPLITS[] = { 1, 2, 3, 4, 6, 8, 12, 16, 24, 32 };
 #define PLAN_CU_FLOPS 0.6e12     /* per-CU steady-state fp32 MFMA rate, FLOP/s */
-#define PLAN_SPLIT_BW 7.37e12    /* effective bytes/s of the partials' round trip */
-#define PLAN_SPLIT_FIXED 2.63e-6 /* reduction launch, s */
-#define PLAN_TAIL 0.045          /* last-round imbalance, in resident-batch durations */
+#define PLAN_SPLIT_BW 1.63e12    /* effective bytes/s of the partials' round trip */
+#define PLAN_SPLIT_FIXED 1.25e-6 /* reduction launch, s */
+#define PLAN_TAIL 0.075          /* last-round imbalance, in resident-batch durations */
 
-static double cu_rate(int c) { return c <= 1 ? 0.742 : 1.0; }
+static double cu_rate(int c) { return c <= 1 ? 0.916 : 1.0; }
 
 static double plan_cost(const PlanTile* pt, int M, int N, int K, u32 batch, int splits) {
     const TileDef* td = &TILES[pt->tile];
