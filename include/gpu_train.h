@@ -51,6 +51,7 @@ typedef struct GpuTrainer {
     HipCtx hip;
     GpuKernels k;
     TrlmGemm* gemm;
+    TrlmGemm* gemm_side;   /* weight-gradient GEMMs on the context's side stream */
 
     u32 V, D, H, L, F, T, B, N, hd;
     f32 eps;

@@ -27,12 +27,14 @@
 #include "trlm_host.h"
 
 typedef struct HipAllocList HipAllocList;
+typedef struct HipSide HipSide;
 
 typedef struct HipCtx {
     i32 device;
     hipModule_t module;
     hipStream_t stream;
     HipAllocList* allocs;
+    HipSide* side;   /* second stream (hip_side_begin), created on first use */
 } HipCtx;
 
 #ifdef __cplusplus
@@ -63,6 +65,19 @@ void hip_sync(void);                                          /* cuda_backend.h:
 
 /* The stream of the context current on this thread (for event timing). */
 hipStream_t hip_current_stream(void);
+
+/* Overlap within one context (not in the reference's backend): a second
+ * stream at default priority.  hip_side_begin() sends the current context's
+ * later launches to it, ordered after everything already queued on the main
+ * stream; hip_side_end(mark) sends launches back to the main stream and
+ * records mark (0..HIP_SIDE_MARKS-1) on the side stream; hip_main_wait(mark)
+ * makes the main stream wait for the side work up to that mark (a mark never
+ * recorded is already reached).  hip_sync and hip_free also wait for the
+ * side stream. */
+#define HIP_SIDE_MARKS 8
+void hip_side_begin(void);
+void hip_side_end(i32 mark);
+void hip_main_wait(i32 mark);
 
 #ifdef __cplusplus
 }

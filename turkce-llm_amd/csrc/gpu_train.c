@@ -61,13 +61,19 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
 /* Weight and bias gradient of a linear layer in one GEMM:
  * dW [M, N] = X^T @ dY (TN, X [K=rows, M], dY [rows, N]) and db [N] =
  * column sums of dY, which the GEMM adds up from the dY tiles it loads
- * (model/gpu_train.c:415-432 runs k_colsum_acc separately). */
-static void gemm_wb(GpuTrainer* g, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW, hipDeviceptr_t db, i32 M,
-                    i32 N, i32 K) {
+ * (model/gpu_train.c:415-432 runs k_colsum_acc separately).
+ * Runs on the side stream, after the main stream's work so far; side mark
+ * `mark` is reached when it is done.  Nothing on the main stream reads
+ * dW / db before the backward's final join; the caller makes the main
+ * stream wait for the mark before it next overwrites dY. */
+static void gemm_wb_side(GpuTrainer* g, i32 mark, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW,
+                         hipDeviceptr_t db, i32 M, i32 N, i32 K) {
     TrlmGemmExtra x;
     memset(&x, 0, sizeof(x));
     x.csum = db;
-    trlm_gemm_ex(g->gemm, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, &x);
+    hip_side_begin();
+    trlm_gemm_ex(g->gemm_side, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, &x);
+    hip_side_end(mark);
 }
 
 /* threads of k_swiglu_fwd / k_swiglu_bwd: one float4 each when F % 4 == 0 */
@@ -259,11 +265,14 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
 static void bind(GpuTrainer* g) {
     hip_set_current(&g->hip);
     if (!g->gemm) g->gemm = trlm_gemm_create(&g->hip);
+    if (!g->gemm_side) g->gemm_side = trlm_gemm_create(&g->hip);
 }
 
 void gpu_trainer_destroy(GpuTrainer* g) {
     hip_set_current(&g->hip);
+    hip_sync();
     if (g->gemm) { trlm_gemm_destroy(g->gemm); g->gemm = NULL; }
+    if (g->gemm_side) { trlm_gemm_destroy(g->gemm_side); g->gemm_side = NULL; }
     hip_shutdown(&g->hip);   /* frees every buffer allocated for this trainer */
 }
 
@@ -466,22 +475,27 @@ static void backward_pass(GpuTrainer* g) {
     AttnParams ap = attn_params(g);
     ap.rope_cos = (const float*)g->cos_t;   /* dQ, dK rotated back as they are stored */
     ap.rope_sin = (const float*)g->sin_t;
+    /* The weight-gradient GEMMs run on the side stream, overlapping the
+     * main stream's dX chain; side marks guard the buffers they read: */
+    enum { MK_DOWN = 0, MK_GU, MK_O, MK_QKV };
     for (i32 l = (i32)g->L - 1; l >= 0; l--) {
         GpuLayerActs* a = &g->layers[l];
         u32 ul = (u32)l;
         /* FFN: x3 = x2 + (h @ Wd + bd); dres = dx3 */
-        gemm_wb(g, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), G_(g, pidx(ul, PK_BDOWN)), F, D, N);
+        gemm_wb_side(g, MK_DOWN, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), G_(g, pidx(ul, PK_BDOWN)), F, D, N);
         gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WDOWN)), g->dh, N, F, D, D, D, F, 0.0f, NULL, NULL);
+        hip_main_wait(MK_GU);   /* the previous layer's dWgu has read dgu */
         {
             hipDeviceptr_t gu = a->gu, dh = g->dh, dgu = g->dgu;
             void* args[] = { &gu, &dh, &dgu, &N, &F };
             hip_launch(g->k.swiglu_bwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);
         }
-        gemm_wb(g, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), G_(g, pidx(ul, PK_BGU)), D, 2 * F, N);
+        gemm_wb_side(g, MK_GU, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), G_(g, pidx(ul, PK_BGU)), D, 2 * F, N);
         gemm1(g, GEMM_NT, g->dgu, P_(g, pidx(ul, PK_WGU)), g->dn, N, D, 2 * F, 2 * F, 2 * F, D, 0.0f, NULL, NULL);
+        hip_main_wait(MK_DOWN);  /* dWdown has read dres */
         rmsnorm_bwd(g, a->x2, P_(g, pidx(ul, PK_FFN_NORM)), a->r2, g->dn, g->dres, G_(g, pidx(ul, PK_FFN_NORM)));
         /* attention: x2 = x + (att @ Wo + bo); dres = dx2 */
-        gemm_wb(g, a->att, g->dres, G_(g, pidx(ul, PK_WO)), G_(g, pidx(ul, PK_BO)), D, D, N);
+        gemm_wb_side(g, MK_O, a->att, g->dres, G_(g, pidx(ul, PK_WO)), G_(g, pidx(ul, PK_BO)), D, D, N);
         gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
         ap.qkv = (const float*)a->qkv; ap.O = (const float*)a->att; ap.dO = (const float*)g->datt;
         ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
@@ -490,15 +504,19 @@ static void backward_pass(GpuTrainer* g) {
             /* D, then dK/dV (leaving dS), then dQ from dS */
             void* args[] = { &ap };
             hip_launch(g->k.attn_dvec, cdiv_u64((u64)g->N * g->D / 4, 256), 1, 1, 256, 1, 1, 0, args);
+            hip_main_wait(MK_QKV);   /* the previous layer's dWqkv has read dqkv */
             hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
             hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
-        gemm_wb(g, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
+        gemm_wb_side(g, MK_QKV, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
         gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,
               NULL);
+        hip_main_wait(MK_O);   /* dWo has read dres */
         rmsnorm_bwd(g, a->x_in, P_(g, pidx(ul, PK_ATTN_NORM)), a->r1, g->dn, g->dres,
                     G_(g, pidx(ul, PK_ATTN_NORM)));
     }
+    /* join: every weight gradient is complete before anything reads it */
+    hip_main_wait(MK_QKV);
     /* embedding: dE[tok] += rows of dres, per token in ascending row order */
     {
         hipDeviceptr_t dx = g->dres, order = g->emb_order, seg = g->emb_seg, dE = G_(g, 0);

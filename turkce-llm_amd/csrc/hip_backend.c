@@ -18,6 +18,13 @@ struct HipAllocList {
     u64 cap;
 };
 
+struct HipSide {
+    hipStream_t stream;
+    hipEvent_t fork;
+    hipEvent_t mark[HIP_SIDE_MARKS];
+    i32 active;
+};
+
 static _Thread_local HipCtx* tls_ctx = NULL;
 
 static void fatal_exit(void) {
@@ -95,12 +102,21 @@ void hip_shutdown(HipCtx* c) {
     if (!c->allocs) return;
     check(hipSetDevice(c->device), "hipSetDevice");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->side) check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
     for (u64 i = 0; i < c->allocs->count; i++)
         if (c->allocs->ptrs[i]) check(hipFree(c->allocs->ptrs[i]), "hipFree");
     free(c->allocs->ptrs);
     pthread_mutex_destroy(&c->allocs->lock);
     free(c->allocs);
     c->allocs = NULL;
+    if (c->side) {
+        check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
+        for (i32 i = 0; i < HIP_SIDE_MARKS; i++) check(hipEventDestroy(c->side->mark[i]), "hipEventDestroy");
+        check(hipEventDestroy(c->side->fork), "hipEventDestroy");
+        check(hipStreamDestroy(c->side->stream), "hipStreamDestroy");
+        free(c->side);
+        c->side = NULL;
+    }
     check(hipStreamDestroy(c->stream), "hipStreamDestroy");
     check(hipModuleUnload(c->module), "hipModuleUnload");
     if (tls_ctx == c) tls_ctx = NULL;
@@ -156,6 +172,7 @@ void hip_free(hipDeviceptr_t p) {
     }
     pthread_mutex_unlock(&l->lock);
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->side) check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
     check(hipFree(p), "hipFree");
 }
 
@@ -175,8 +192,44 @@ void hip_launch(hipFunction_t f, u32 gx, u32 gy, u32 gz, u32 bx, u32 by, u32 bz,
                 void** params) {
     HipCtx* c = current("hip_launch");
     if (gx == 0 || gy == 0 || gz == 0) return;
-    check(hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, shared_bytes, c->stream, params, NULL),
+    hipStream_t st = (c->side && c->side->active) ? c->side->stream : c->stream;
+    check(hipModuleLaunchKernel(f, gx, gy, gz, bx, by, bz, shared_bytes, st, params, NULL),
           "hipModuleLaunchKernel");
+}
+
+void hip_side_begin(void) {
+    HipCtx* c = current("hip_side_begin");
+    if (!c->side) {
+        HipSide* s = (HipSide*)calloc(1, sizeof(HipSide));
+        check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
+        check(hipEventCreateWithFlags(&s->fork, hipEventDisableTiming), "hipEventCreateWithFlags");
+        for (i32 i = 0; i < HIP_SIDE_MARKS; i++)
+            check(hipEventCreateWithFlags(&s->mark[i], hipEventDisableTiming), "hipEventCreateWithFlags");
+        c->side = s;
+    }
+    check(hipEventRecord(c->side->fork, c->stream), "hipEventRecord");
+    check(hipStreamWaitEvent(c->side->stream, c->side->fork, 0), "hipStreamWaitEvent");
+    c->side->active = 1;
+}
+
+static HipSide* side_of(HipCtx* c, i32 mark, const char* what) {
+    if (!c->side || mark < 0 || mark >= HIP_SIDE_MARKS) {
+        fprintf(stderr, "[HIP ERROR] %s: no side stream or mark %d out of range\n", what, mark);
+        fatal_exit();
+    }
+    return c->side;
+}
+
+void hip_side_end(i32 mark) {
+    HipSide* s = side_of(current("hip_side_end"), mark, "hip_side_end");
+    check(hipEventRecord(s->mark[mark], s->stream), "hipEventRecord");
+    s->active = 0;
+}
+
+void hip_main_wait(i32 mark) {
+    HipCtx* c = current("hip_main_wait");
+    HipSide* s = side_of(c, mark, "hip_main_wait");
+    check(hipStreamWaitEvent(c->stream, s->mark[mark], 0), "hipStreamWaitEvent");
 }
 
 #define BLOCK_1D 256u
@@ -204,4 +257,5 @@ void hip_memset_zero(hipDeviceptr_t p, u64 bytes) {
 void hip_sync(void) {
     HipCtx* c = current("hip_sync");
     check(hipStreamSynchronize(c->stream), "hipStreamSynchronize");
+    if (c->side) check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
 }

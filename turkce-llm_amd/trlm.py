@@ -79,7 +79,8 @@ class PCGState(C.Structure):
 
 
 class HipCtx(C.Structure):
-    _fields_ = [("device", C.c_int32), ("module", C.c_void_p), ("stream", C.c_void_p), ("allocs", C.c_void_p)]
+    _fields_ = [("device", C.c_int32), ("module", C.c_void_p), ("stream", C.c_void_p), ("allocs", C.c_void_p),
+                ("side", C.c_void_p)]
 
 
 class TrlmTimer(C.Structure):
