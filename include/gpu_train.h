@@ -67,6 +67,8 @@ typedef struct GpuTrainer {
     hipDeviceptr_t x_final, nf, rf, logits;   /* logits [N, ldv]: gradient after the CE */
 
     hipDeviceptr_t dres, dn, datt, dqkv, dh, dgu, dvec, part;
+    hipDeviceptr_t part2;                     /* RMSNorm partials: part / part2 alternate */
+    u32 norm_seq;                             /* RMSNorm backwards issued in this backward */
     hipDeviceptr_t att_ds;                    /* attention backward: causal dS blocks of one layer */
 
     hipDeviceptr_t ids, targets, loss_rows, cos_t, sin_t;

@@ -72,12 +72,13 @@ hipStream_t hip_current_stream(void);
  * stream; hip_side_end(mark) sends launches back to the main stream and
  * records mark (0..HIP_SIDE_MARKS-1) on the side stream; hip_main_wait(mark)
  * makes the main stream wait for the side work up to that mark (a mark never
- * recorded is already reached).  hip_sync and hip_free also wait for the
- * side stream. */
+ * recorded is already reached); hip_side_join() makes it wait for all side
+ * work queued so far.  hip_sync and hip_free also wait for the side stream. */
 #define HIP_SIDE_MARKS 8
 void hip_side_begin(void);
 void hip_side_end(i32 mark);
 void hip_main_wait(i32 mark);
+void hip_side_join(void);
 
 #ifdef __cplusplus
 }

@@ -98,16 +98,23 @@ static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
 #define RMS_ROWS 16u
 
 /* dx += RMSNorm backward; dw = sum over rows of dy*x*r  (gpu_train.c:132-140) */
+/* The weight gradient's final column sum runs on the side stream (marks 5
+ * and 6), off the dX chain; the partial buffers alternate, and the main
+ * stream waits for a buffer's previous sum before refilling it. */
 static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t rinv, hipDeviceptr_t dy,
                         hipDeviceptr_t dx, hipDeviceptr_t dw) {
     i32 rows = (i32)g->N, cols = (i32)g->D;
-    hipDeviceptr_t part = g->part;
+    const i32 which = (i32)(g->norm_seq++ & 1u), mark = 5 + which;
+    hipDeviceptr_t part = which ? g->part2 : g->part;
     u32 nb = cdiv_u64(g->N, RMS_ROWS);
     void* args[] = { &x, &w, &rinv, &dy, &dx, &part, &rows, &cols };
+    hip_main_wait(mark);
     hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
     i32 inb = (i32)nb, acc = 0;
     void* args2[] = { &part, &inb, &cols, &dw, &acc };
+    hip_side_begin();
     hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
+    hip_side_end(mark);
 }
 
 /* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
@@ -207,6 +214,7 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     }
     u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;   /* RMSNorm weight-gradient partials */
     g.part = dalloc(part_rows * D);
+    g.part2 = dalloc(part_rows * D);
 
     g.ids = hip_alloc(N * sizeof(u32));
     g.targets = hip_alloc(N * sizeof(u32));
@@ -476,7 +484,8 @@ static void backward_pass(GpuTrainer* g) {
     ap.rope_cos = (const float*)g->cos_t;   /* dQ, dK rotated back as they are stored */
     ap.rope_sin = (const float*)g->sin_t;
     /* The weight-gradient GEMMs run on the side stream, overlapping the
-     * main stream's dX chain; side marks guard the buffers they read: */
+     * main stream's dX chain; side marks guard the buffers they read (marks
+     * 5 and 6 belong to rmsnorm_bwd): */
     enum { MK_DOWN = 0, MK_GU, MK_O, MK_QKV };
     for (i32 l = (i32)g->L - 1; l >= 0; l--) {
         GpuLayerActs* a = &g->layers[l];
@@ -516,7 +525,7 @@ static void backward_pass(GpuTrainer* g) {
                     G_(g, pidx(ul, PK_ATTN_NORM)));
     }
     /* join: every weight gradient is complete before anything reads it */
-    hip_main_wait(MK_QKV);
+    hip_side_join();
     /* embedding: dE[tok] += rows of dres, per token in ascending row order */
     {
         hipDeviceptr_t dx = g->dres, order = g->emb_order, seg = g->emb_seg, dE = G_(g, 0);

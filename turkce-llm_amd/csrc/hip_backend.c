@@ -20,7 +20,7 @@ struct HipAllocList {
 
 struct HipSide {
     hipStream_t stream;
-    hipEvent_t fork;
+    hipEvent_t fork, join;
     hipEvent_t mark[HIP_SIDE_MARKS];
     i32 active;
 };
@@ -113,6 +113,7 @@ void hip_shutdown(HipCtx* c) {
         check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
         for (i32 i = 0; i < HIP_SIDE_MARKS; i++) check(hipEventDestroy(c->side->mark[i]), "hipEventDestroy");
         check(hipEventDestroy(c->side->fork), "hipEventDestroy");
+        check(hipEventDestroy(c->side->join), "hipEventDestroy");
         check(hipStreamDestroy(c->side->stream), "hipStreamDestroy");
         free(c->side);
         c->side = NULL;
@@ -203,6 +204,7 @@ void hip_side_begin(void) {
         HipSide* s = (HipSide*)calloc(1, sizeof(HipSide));
         check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
         check(hipEventCreateWithFlags(&s->fork, hipEventDisableTiming), "hipEventCreateWithFlags");
+        check(hipEventCreateWithFlags(&s->join, hipEventDisableTiming), "hipEventCreateWithFlags");
         for (i32 i = 0; i < HIP_SIDE_MARKS; i++)
             check(hipEventCreateWithFlags(&s->mark[i], hipEventDisableTiming), "hipEventCreateWithFlags");
         c->side = s;
@@ -212,24 +214,36 @@ void hip_side_begin(void) {
     c->side->active = 1;
 }
 
-static HipSide* side_of(HipCtx* c, i32 mark, const char* what) {
-    if (!c->side || mark < 0 || mark >= HIP_SIDE_MARKS) {
-        fprintf(stderr, "[HIP ERROR] %s: no side stream or mark %d out of range\n", what, mark);
+static void check_mark(i32 mark, const char* what) {
+    if (mark < 0 || mark >= HIP_SIDE_MARKS) {
+        fprintf(stderr, "[HIP ERROR] %s: side mark %d out of range\n", what, mark);
         fatal_exit();
     }
-    return c->side;
 }
 
 void hip_side_end(i32 mark) {
-    HipSide* s = side_of(current("hip_side_end"), mark, "hip_side_end");
-    check(hipEventRecord(s->mark[mark], s->stream), "hipEventRecord");
-    s->active = 0;
+    HipCtx* c = current("hip_side_end");
+    check_mark(mark, "hip_side_end");
+    if (!c->side || !c->side->active) {
+        fprintf(stderr, "[HIP ERROR] hip_side_end without hip_side_begin\n");
+        fatal_exit();
+    }
+    check(hipEventRecord(c->side->mark[mark], c->side->stream), "hipEventRecord");
+    c->side->active = 0;
 }
 
 void hip_main_wait(i32 mark) {
     HipCtx* c = current("hip_main_wait");
-    HipSide* s = side_of(c, mark, "hip_main_wait");
-    check(hipStreamWaitEvent(c->stream, s->mark[mark], 0), "hipStreamWaitEvent");
+    check_mark(mark, "hip_main_wait");
+    if (!c->side) return;   /* nothing was ever queued on the side stream */
+    check(hipStreamWaitEvent(c->stream, c->side->mark[mark], 0), "hipStreamWaitEvent");
+}
+
+void hip_side_join(void) {
+    HipCtx* c = current("hip_side_join");
+    if (!c->side) return;
+    check(hipEventRecord(c->side->join, c->side->stream), "hipEventRecord");
+    check(hipStreamWaitEvent(c->stream, c->side->join, 0), "hipStreamWaitEvent");
 }
 
 #define BLOCK_1D 256u
