@@ -561,7 +561,6 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
                     }
                 }
             }
-            __builtin_amdgcn_s_setprio(1);
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -569,7 +568,17 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
 #pragma unroll
                     for (int j = 0; j < FN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u][j][s], fa[u][i][s], acc[i][j], 0, 0, 0);
-            __builtin_amdgcn_s_setprio(0);
+            // Spread this chunk's memory instructions between its MFMAs:
+            // groups of 3 MFMAs, 1 LDS read, 1 global load, 1 LDS write
+            // (+2-4 % on the LM-head GEMMs against issuing them in one run
+            // beside a raised wave priority).
+#pragma unroll
+            for (int q = 0; q < FM * FN; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // MFMA
+                __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
+                __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
+                __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
+            }
         }
     };
     for (int kt = 0; kt < nk; kt += 2) {
