@@ -569,12 +569,14 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
                     for (int j = 0; j < FN; j++)
                         acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x2f32(fb[u][j][s], fa[u][i][s], acc[i][j], 0, 0, 0);
             // Spread this chunk's memory instructions between its MFMAs:
-            // groups of 3 MFMAs, 1 LDS read, 1 global load, 1 LDS write
-            // (+2-4 % on the LM-head GEMMs against issuing them in one run
-            // beside a raised wave priority).
+            // groups of SG MFMAs (2 for the 16-MFMA chunks of 128x128, else
+            // 1), 1 LDS read, 1 global load, 1 LDS write (+2-4 % on the
+            // LM-head GEMMs against issuing them in one run beside a raised
+            // wave priority; the group size measured best per tile).
+            constexpr int SG = FM * FN >= 4 ? 2 : 1;
 #pragma unroll
-            for (int q = 0; q < FM * FN; q++) {
-                __builtin_amdgcn_sched_group_barrier(0x008, 3, 0);   // MFMA
+            for (int q = 0; q < 4 * FM * FN / SG; q++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, SG, 0);  // MFMA
                 __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // LDS read
                 __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);   // global load
                 __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);   // LDS write
