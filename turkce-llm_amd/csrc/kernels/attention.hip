@@ -298,6 +298,12 @@ __device__ void flash_fwd(const AttnParams& p) {
                 for (int t = 0; t < 4; t++) s[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[j][t], s[c], 0, 0, 0);
             }
         }
+        // one K-fragment read between consecutive groups of 4 MFMAs
+#pragma unroll
+        for (int q = 0; q < HD / 4; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
         // Causal mask on the diagonal block only (the block index is
         // wave-uniform); the max is taken on the raw scores (the scale is
         // positive) and the scale folds into the exponent's FMA.  Every
@@ -356,6 +362,12 @@ __device__ void flash_fwd(const AttnParams& p) {
                     for (int d = 0; d < DB; d++)
                         o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[d][t], s[c][4 * g + t], o[d], 0, 0, 0);
             }
+        // one V^T-fragment read between consecutive groups of 4 MFMAs
+#pragma unroll
+        for (int q = 0; q < 8 * DB; q++) {
+            __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+            __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
+        }
     }
     // merge the two key partitions of each query group: (m, l, O) of part 1
     // go through LDS to the part-0 wave, which rescales, adds and stores.
