@@ -376,11 +376,11 @@ void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_l
     hipDeviceptr_t lg = d->logits, ids = d->ids, hist = d->hist, posd = d->pos_dev;
     i32 ld = (i32)d->ldv, V = (i32)d->V, hl = (i32)steps, base = (i32)prompt_len;
     void* args[] = { &lg, &ld, &V, &ids, &hist, &hl, &posd, &base };
-    hip_launch(d->k_argmax_hist, d->B, 1, 1, 256, 1, 1, 0, args);
+    hip_launch(d->k_argmax_hist, d->B, 1, 1, 1024, 1, 1, 0, args);
     for (u32 s = 1; s < steps; s++) {
         run_step(d);
         d->len++;
-        hip_launch(d->k_argmax_hist, d->B, 1, 1, 256, 1, 1, 0, args);
+        hip_launch(d->k_argmax_hist, d->B, 1, 1, 1024, 1, 1, 0, args);
     }
     hip_d2h(out, d->hist, (u64)d->B * steps * sizeof(u32));
 }

@@ -209,17 +209,31 @@ extern "C" __global__ void k_decode_advance(int* __restrict__ pos_dev) {
 // Greedy pick per row (first index of the maximum, as k_argmax_rows), written
 // both as the next step's input ids[row] and into hist[row*hist_ld + step]
 // with step = *pos_dev - pos_base, so generation needs no host round trip.
-extern "C" __global__ void __launch_bounds__(256)
+#define ARGMAX_THREADS 1024
+extern "C" __global__ void __launch_bounds__(ARGMAX_THREADS)
 k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restrict__ ids,
               unsigned* __restrict__ hist, int hist_ld, const int* __restrict__ pos_dev, int pos_base) {
-    __shared__ float bv[4];
-    __shared__ int bi[4];
+    constexpr int NW = ARGMAX_THREADS / 64;
+    __shared__ float bv[NW];
+    __shared__ int bi[NW];
     const float* z = logits + (long long)blockIdx.x * ld;
     float best = -INFINITY;
     int idx = 0x7fffffff;
-    for (int j = threadIdx.x; j < V; j += 256) {
-        float v = z[j];
-        if (v > best) { best = v; idx = j; }
+    // each thread scans its float4s in increasing index order, strict > keeps
+    // the first occurrence; the reductions prefer the lower index on ties
+    if ((ld & 3) == 0) {
+        const int nq = V >> 2;
+        for (int q = threadIdx.x; q < nq; q += ARGMAX_THREADS) {
+            const f32x4 v = *(const f32x4*)(z + 4 * q);
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                if (v[e] > best) { best = v[e]; idx = 4 * q + e; }
+        }
+        for (int j = 4 * nq + (int)threadIdx.x; j < V; j += ARGMAX_THREADS)
+            if (z[j] > best) { best = z[j]; idx = j; }
+    } else {
+        for (int j = threadIdx.x; j < V; j += ARGMAX_THREADS)
+            if (z[j] > best) { best = z[j]; idx = j; }
     }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) {
@@ -233,7 +247,7 @@ k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restr
     if (threadIdx.x == 0) {
         float b = bv[0];
         int k = bi[0];
-        for (int w = 1; w < 4; w++)
+        for (int w = 1; w < NW; w++)
             if (bv[w] > b || (bv[w] == b && bi[w] < k)) { b = bv[w]; k = bi[w]; }
         ids[blockIdx.x] = (unsigned)k;
         hist[(long long)blockIdx.x * hist_ld + (*pos_dev - pos_base)] = (unsigned)k;
