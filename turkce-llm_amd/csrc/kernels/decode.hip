@@ -102,17 +102,25 @@ __device__ void decode_attn(const float* __restrict__ qkv, int ldq, const float*
     const long long cbase = ((long long)bh * ctx) * HD;
     const f32x4 q = *(const f32x4*)(qkv + (long long)b * ldq + h * HD + 4 * c4);
 
-    // scores
-    for (int j0 = wave * RPI; j0 < cnt; j0 += 4 * RPI) {
-        const int j = j0 + sub;
-        float d = 0.f;
-        if (j < cnt) {
-            f32x4 kv = *(const f32x4*)(kc + cbase + (long long)(k0 + j) * HD + 4 * c4);
-            d = kv[0] * q[0] + kv[1] * q[1] + kv[2] * q[2] + kv[3] * q[3];
+    // scores: a wave's rows of NIT iterations are loaded together (their
+    // latency overlaps), then reduced across the LPR lanes of each row
+    constexpr int NIT = 256 / (4 * RPI);
+    for (int g0 = 0; g0 < cnt; g0 += NIT * 4 * RPI) {
+        f32x4 kv[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
+            kv[it] = j < cnt ? *(const f32x4*)(kc + cbase + (long long)(k0 + j) * HD + 4 * c4)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
         }
 #pragma unroll
-        for (int o = 1; o < LPR; o <<= 1) d += __shfl_xor(d, o, WAVE);
-        if (c4 == 0 && j < cnt) sc[j] = d * c2;
+        for (int it = 0; it < NIT; it++) {
+            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
+            float d = kv[it][0] * q[0] + kv[it][1] * q[1] + kv[it][2] * q[2] + kv[it][3] * q[3];
+#pragma unroll
+            for (int o = 1; o < LPR; o <<= 1) d += __shfl_xor(d, o, WAVE);
+            if (c4 == 0 && j < cnt) sc[j] = d * c2;
+        }
     }
     __syncthreads();
     // max and sum of 2^(score - max) over the chunk (fixed order)
@@ -133,11 +141,18 @@ __device__ void decode_attn(const float* __restrict__ qkv, int ldq, const float*
     __syncthreads();
     // O = sum_j p_j V_j
     f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int j0 = wave * RPI; j0 < cnt; j0 += 4 * RPI) {
-        const int j = j0 + sub;
-        if (j < cnt) {
-            f32x4 vv = *(const f32x4*)(vc + cbase + (long long)(k0 + j) * HD + 4 * c4);
-            o += sc[j] * vv;
+    for (int g0 = 0; g0 < cnt; g0 += NIT * 4 * RPI) {
+        f32x4 vv[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
+            vv[it] = j < cnt ? *(const f32x4*)(vc + cbase + (long long)(k0 + j) * HD + 4 * c4)
+                             : f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
+            if (j < cnt) o += sc[j] * vv[it];
         }
     }
 #pragma unroll
