@@ -23,6 +23,7 @@
 
 #define GPU_TRAIN_MAX_PARAMS (LM_MAX_LAYERS * 10u + 2u)
 #define GPU_TRAIN_NORM_BLOCKS 1024u
+#define GPU_TRAIN_DRES_RING 5u   /* residual-gradient versions live at once in the backward */
 
 typedef struct GpuLayerActs {
     hipDeviceptr_t x_in;   /* [N,D] layer input (residual stream) */
@@ -41,7 +42,7 @@ typedef struct GpuLayerActs {
 typedef struct TrlmGemm TrlmGemm;
 
 typedef struct GpuKernels {
-    hipFunction_t fill_zero, embed_fwd, embed_bwd, rmsnorm_fwd, rmsnorm_bwd, colsum_final;
+    hipFunction_t embed_fwd, embed_bwd, rmsnorm_fwd, rmsnorm_bwd, colsum_final;
     hipFunction_t swiglu_fwd, swiglu_bwd, cross_entropy, argmax_rows, sumsq_partial, adam;
     hipFunction_t attn_fwd, attn_bwd_dkv, attn_bwd_dq, attn_dvec;
     hipFunction_t loss_mean, norm_clip, adam_ds;   /* queued driver steps (trlm_ext.h) */
@@ -66,9 +67,16 @@ typedef struct GpuTrainer {
     GpuLayerActs layers[LM_MAX_LAYERS];
     hipDeviceptr_t x_final, nf, rf, logits;   /* logits [N, ldv]: gradient after the CE */
 
-    hipDeviceptr_t dres, dn, datt, dqkv, dh, dgu, dvec, part;
-    hipDeviceptr_t part2;                     /* RMSNorm partials: part / part2 alternate */
-    u32 norm_seq;                             /* RMSNorm backwards issued in this backward */
+    /* Backward scratch.  The weight-gradient work of a layer runs on the side
+     * stream while the main stream goes on with the next layer, so what it
+     * reads is kept apart from what the next layer writes: the residual
+     * gradient moves through a ring of versions (two per layer), and dqkv,
+     * dgu and the RMSNorm weight partials alternate by layer parity. */
+    hipDeviceptr_t dres[GPU_TRAIN_DRES_RING];
+    hipDeviceptr_t dqkv[2], dgu[2];
+    hipDeviceptr_t part[2][2];                /* [layer parity][attention / FFN norm] */
+    hipDeviceptr_t part_final;                /* the final norm's partials */
+    hipDeviceptr_t dn, datt, dh, dvec;
     hipDeviceptr_t att_ds;                    /* attention backward: causal dS blocks of one layer */
 
     hipDeviceptr_t ids, targets, loss_rows, cos_t, sin_t;

@@ -40,15 +40,6 @@ static void fatal(const char* msg) {
 
 static u32 cdiv_u64(u64 a, u64 b) { return (u32)((a + b - 1) / b); }
 
-static void fill_zero(GpuTrainer* g, hipDeviceptr_t p, u64 n) {
-    long long nn = (long long)n;
-    void* args[] = { &p, &nn };
-    u32 grid = cdiv_u64(n, 256);
-    if (grid > 4096) grid = 4096;
-    if (grid == 0) return;
-    hip_launch(g->k.fill_zero, grid, 1, 1, 256, 1, 1, 0, args);
-}
-
 /* C[M,N] = op(A) op(B) (+ beta C) (+ bias) (+ resid), single matrices with
  * the reference's leading-dimension conventions (gpu_train.c:53-63). */
 
@@ -61,19 +52,14 @@ static void gemm1(GpuTrainer* g, GemmKind kind, hipDeviceptr_t A, hipDeviceptr_t
 /* Weight and bias gradient of a linear layer in one GEMM:
  * dW [M, N] = X^T @ dY (TN, X [K=rows, M], dY [rows, N]) and db [N] =
  * column sums of dY, which the GEMM adds up from the dY tiles it loads
- * (model/gpu_train.c:415-432 runs k_colsum_acc separately).
- * Runs on the side stream, after the main stream's work so far; side mark
- * `mark` is reached when it is done.  Nothing on the main stream reads
- * dW / db before the backward's final join; the caller makes the main
- * stream wait for the mark before it next overwrites dY. */
-static void gemm_wb_side(GpuTrainer* g, i32 mark, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW,
-                         hipDeviceptr_t db, i32 M, i32 N, i32 K) {
+ * (model/gpu_train.c:415-432 runs k_colsum_acc separately).  Issued inside
+ * a side-stream section, on the side GEMM context. */
+static void gemm_wb(GpuTrainer* g, hipDeviceptr_t X, hipDeviceptr_t dY, hipDeviceptr_t dW, hipDeviceptr_t db, i32 M,
+                    i32 N, i32 K) {
     TrlmGemmExtra x;
     memset(&x, 0, sizeof(x));
     x.csum = db;
-    hip_side_begin();
     trlm_gemm_ex(g->gemm_side, 1, 0, X, dY, dW, M, N, K, M, N, N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, N, &x);
-    hip_side_end(mark);
 }
 
 /* threads of k_swiglu_fwd / k_swiglu_bwd: one float4 each when F % 4 == 0 */
@@ -101,20 +87,22 @@ static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
 /* The weight gradient's final column sum runs on the side stream (marks 5
  * and 6), off the dX chain; the partial buffers alternate, and the main
  * stream waits for a buffer's previous sum before refilling it. */
+/* RMSNorm backward on the current stream: dx = dxin (zero when dxin is 0) +
+ * the norm's input gradient, and the weight gradient's per-block partials
+ * into part (rows in order; colsum_partials adds them up). */
 static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t rinv, hipDeviceptr_t dy,
-                        hipDeviceptr_t dx, hipDeviceptr_t dw) {
+                        hipDeviceptr_t dxin, hipDeviceptr_t dx, hipDeviceptr_t part) {
     i32 rows = (i32)g->N, cols = (i32)g->D;
-    const i32 which = (i32)(g->norm_seq++ & 1u), mark = 5 + which;
-    hipDeviceptr_t part = which ? g->part2 : g->part;
     u32 nb = cdiv_u64(g->N, RMS_ROWS);
-    void* args[] = { &x, &w, &rinv, &dy, &dx, &part, &rows, &cols };
-    hip_main_wait(mark);
+    void* args[] = { &x, &w, &rinv, &dy, &dxin, &dx, &part, &rows, &cols };
     hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
-    i32 inb = (i32)nb, acc = 0;
-    void* args2[] = { &part, &inb, &cols, &dw, &acc };
-    hip_side_begin();
-    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args2);
-    hip_side_end(mark);
+}
+
+/* dw = sum of an RMSNorm backward's partial rows, in block order. */
+static void colsum_partials(GpuTrainer* g, hipDeviceptr_t part, hipDeviceptr_t dw) {
+    i32 inb = (i32)cdiv_u64(g->N, RMS_ROWS), cols = (i32)g->D, acc = 0;
+    void* args[] = { &part, &inb, &cols, &dw, &acc };
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args);
 }
 
 /* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
@@ -201,20 +189,22 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.ce_stats_cap = 2 * (i32)((g.V + 63) / 64);     /* two entries per 64-wide (smallest) tile column */
     g.ce_stats = dalloc(N * (u64)g.ce_stats_cap * 2);
 
-    g.dres = dalloc(N * D);
+    for (u32 i = 0; i < GPU_TRAIN_DRES_RING; i++) g.dres[i] = dalloc(N * D);
     g.dn = dalloc(N * D);
     g.datt = dalloc(N * D);
-    g.dqkv = dalloc(N * 3 * D);
     g.dh = dalloc(N * F);
-    g.dgu = dalloc(N * 2 * F);
+    for (u32 i = 0; i < 2; i++) {
+        g.dqkv[i] = dalloc(N * 3 * D);
+        g.dgu[i] = dalloc(N * 2 * F);
+    }
     g.dvec = dalloc(BHT);
     {
         u64 nqb = ((u64)g.T + 63) / 64;
         g.att_ds = dalloc((u64)g.B * g.H * (nqb * (nqb + 1) / 2) * 4096);
     }
     u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;   /* RMSNorm weight-gradient partials */
-    g.part = dalloc(part_rows * D);
-    g.part2 = dalloc(part_rows * D);
+    for (u32 i = 0; i < 4; i++) g.part[i / 2][i % 2] = dalloc(part_rows * D);
+    g.part_final = dalloc(part_rows * D);
 
     g.ids = hip_alloc(N * sizeof(u32));
     g.targets = hip_alloc(N * sizeof(u32));
@@ -238,7 +228,6 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     hip_h2d(g.sin_t, sin_t.data, sin_t.numel * F4);
 
     HipCtx* c = &g.hip;
-    g.k.fill_zero = hip_get_kernel(c, "k_fill_zero");
     g.k.embed_fwd = hip_get_kernel(c, "k_embed_fwd");
     g.k.embed_bwd = hip_get_kernel(c, "k_embed_bwd");
     g.k.rmsnorm_fwd = hip_get_kernel(c, "k_rmsnorm_fwd");
@@ -473,62 +462,81 @@ static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
 static void backward_pass(GpuTrainer* g) {
     i32 N = (i32)g->N, D = (i32)g->D, F = (i32)g->F, V = (i32)g->V, ldv = (i32)g->ldv;
     u32 p_final = pidx(g->L, 0);
+    const u32 R = GPU_TRAIN_DRES_RING;
 
-    /* tied head: dE = dlogits^T @ nf ; dnf = dlogits @ E */
-    gemm1(g, GEMM_TN, g->logits, g->nf, G_(g, 0), V, D, N, ldv, D, D, 0.0f, NULL, NULL);
+    /* tied head, dnf = dlogits @ E (dE = dlogits^T @ nf comes last, below) */
     gemm1(g, GEMM_NN, g->logits, P_(g, 0), g->dn, N, D, V, ldv, D, D, 0.0f, NULL, NULL);
-    fill_zero(g, g->dres, (u64)N * D);
-    rmsnorm_bwd(g, g->x_final, P_(g, p_final), g->rf, g->dn, g->dres, G_(g, p_final));
+    rmsnorm_bwd(g, g->x_final, P_(g, p_final), g->rf, g->dn, 0, g->dres[0], g->part_final);
 
     AttnParams ap = attn_params(g);
     ap.rope_cos = (const float*)g->cos_t;   /* dQ, dK rotated back as they are stored */
     ap.rope_sin = (const float*)g->sin_t;
-    /* The weight-gradient GEMMs run on the side stream, overlapping the
-     * main stream's dX chain; side marks guard the buffers they read (marks
-     * 5 and 6 belong to rmsnorm_bwd): */
-    enum { MK_DOWN = 0, MK_GU, MK_O, MK_QKV };
+    /* The weight gradients (GEMMs with their bias sums, norm-weight sums)
+     * run on the side stream, each section issued as soon as the main
+     * stream's dX chain has produced what it reads, so it overlaps the
+     * chain's next kernels.  What the sections of layer step j read -- its
+     * two residual-gradient versions, dgu, dqkv and the norm partials of its
+     * parity -- is next written in step j + 2, which first waits for side
+     * mark 0: the end of step j + 1's first section, issued after all of
+     * step j's. */
+    u32 v = 0;   /* dres[v % R]: gradient at the current layer's output */
+    hipDeviceptr_t part_prev = g->part_final, w_prev = G_(g, p_final);   /* norm partials still to sum */
     for (i32 l = (i32)g->L - 1; l >= 0; l--) {
         GpuLayerActs* a = &g->layers[l];
-        u32 ul = (u32)l;
-        /* FFN: x3 = x2 + (h @ Wd + bd); dres = dx3 */
-        gemm_wb_side(g, MK_DOWN, a->h, g->dres, G_(g, pidx(ul, PK_WDOWN)), G_(g, pidx(ul, PK_BDOWN)), F, D, N);
-        gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WDOWN)), g->dh, N, F, D, D, D, F, 0.0f, NULL, NULL);
-        hip_main_wait(MK_GU);   /* the previous layer's dWgu has read dgu */
+        const u32 ul = (u32)l, step = g->L - 1u - ul, par = step & 1u;
+        hipDeviceptr_t d_out = g->dres[v % R], d_mid = g->dres[(v + 1) % R], d_in = g->dres[(v + 2) % R];
+        hipDeviceptr_t dgu = g->dgu[par], dqkv = g->dqkv[par];
+        if (step >= 2) hip_main_wait(0);
+        /* FFN: x3 = x2 + (h @ Wd + bd); d_out = dx3 */
+        hip_side_begin();
+        colsum_partials(g, part_prev, w_prev);
+        gemm_wb(g, a->h, d_out, G_(g, pidx(ul, PK_WDOWN)), G_(g, pidx(ul, PK_BDOWN)), F, D, N);
+        hip_side_end(0);
+        gemm1(g, GEMM_NT, d_out, P_(g, pidx(ul, PK_WDOWN)), g->dh, N, F, D, D, D, F, 0.0f, NULL, NULL);
         {
-            hipDeviceptr_t gu = a->gu, dh = g->dh, dgu = g->dgu;
+            hipDeviceptr_t gu = a->gu, dh = g->dh;
             void* args[] = { &gu, &dh, &dgu, &N, &F };
             hip_launch(g->k.swiglu_bwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);
         }
-        gemm_wb_side(g, MK_GU, a->n2, g->dgu, G_(g, pidx(ul, PK_WGU)), G_(g, pidx(ul, PK_BGU)), D, 2 * F, N);
-        gemm1(g, GEMM_NT, g->dgu, P_(g, pidx(ul, PK_WGU)), g->dn, N, D, 2 * F, 2 * F, 2 * F, D, 0.0f, NULL, NULL);
-        hip_main_wait(MK_DOWN);  /* dWdown has read dres */
-        rmsnorm_bwd(g, a->x2, P_(g, pidx(ul, PK_FFN_NORM)), a->r2, g->dn, g->dres, G_(g, pidx(ul, PK_FFN_NORM)));
-        /* attention: x2 = x + (att @ Wo + bo); dres = dx2 */
-        gemm_wb_side(g, MK_O, a->att, g->dres, G_(g, pidx(ul, PK_WO)), G_(g, pidx(ul, PK_BO)), D, D, N);
-        gemm1(g, GEMM_NT, g->dres, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
+        hip_side_begin();
+        gemm_wb(g, a->n2, dgu, G_(g, pidx(ul, PK_WGU)), G_(g, pidx(ul, PK_BGU)), D, 2 * F, N);
+        hip_side_end(1);
+        gemm1(g, GEMM_NT, dgu, P_(g, pidx(ul, PK_WGU)), g->dn, N, D, 2 * F, 2 * F, 2 * F, D, 0.0f, NULL, NULL);
+        rmsnorm_bwd(g, a->x2, P_(g, pidx(ul, PK_FFN_NORM)), a->r2, g->dn, d_out, d_mid, g->part[par][1]);
+        /* attention: x2 = x + (att @ Wo + bo); d_mid = dx2 */
+        hip_side_begin();
+        colsum_partials(g, g->part[par][1], G_(g, pidx(ul, PK_FFN_NORM)));
+        gemm_wb(g, a->att, d_mid, G_(g, pidx(ul, PK_WO)), G_(g, pidx(ul, PK_BO)), D, D, N);
+        hip_side_end(2);
+        gemm1(g, GEMM_NT, d_mid, P_(g, pidx(ul, PK_WO)), g->datt, N, D, D, D, D, D, 0.0f, NULL, NULL);
         ap.qkv = (const float*)a->qkv; ap.O = (const float*)a->att; ap.dO = (const float*)g->datt;
-        ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)g->dqkv;
+        ap.lse = (float*)a->lse; ap.dvec = (float*)g->dvec; ap.out = (float*)dqkv;
         ap.ds = (float*)g->att_ds;
         {
             /* D, then dK/dV (leaving dS), then dQ from dS */
             void* args[] = { &ap };
             hip_launch(g->k.attn_dvec, cdiv_u64((u64)g->N * g->D / 4, 256), 1, 1, 256, 1, 1, 0, args);
-            hip_main_wait(MK_QKV);   /* the previous layer's dWqkv has read dqkv */
             hip_launch(g->k.attn_bwd_dkv, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
             hip_launch(g->k.attn_bwd_dq, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);
         }
-        gemm_wb_side(g, MK_QKV, a->n1, g->dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
-        gemm1(g, GEMM_NT, g->dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL,
-              NULL);
-        hip_main_wait(MK_O);   /* dWo has read dres */
-        rmsnorm_bwd(g, a->x_in, P_(g, pidx(ul, PK_ATTN_NORM)), a->r1, g->dn, g->dres,
-                    G_(g, pidx(ul, PK_ATTN_NORM)));
+        hip_side_begin();
+        gemm_wb(g, a->n1, dqkv, G_(g, pidx(ul, PK_WQKV)), G_(g, pidx(ul, PK_BQKV)), D, 3 * D, N);
+        hip_side_end(3);
+        gemm1(g, GEMM_NT, dqkv, P_(g, pidx(ul, PK_WQKV)), g->dn, N, D, 3 * D, 3 * D, 3 * D, D, 0.0f, NULL, NULL);
+        rmsnorm_bwd(g, a->x_in, P_(g, pidx(ul, PK_ATTN_NORM)), a->r1, g->dn, d_mid, d_in, g->part[par][0]);
+        part_prev = g->part[par][0];
+        w_prev = G_(g, pidx(ul, PK_ATTN_NORM));
+        v += 2;
     }
+    colsum_partials(g, part_prev, w_prev);
+    /* tied head: dE = dlogits^T @ nf, overlapping the last side sections */
+    gemm1(g, GEMM_TN, g->logits, g->nf, G_(g, 0), V, D, N, ldv, D, D, 0.0f, NULL, NULL);
     /* join: every weight gradient is complete before anything reads it */
     hip_side_join();
-    /* embedding: dE[tok] += rows of dres, per token in ascending row order */
+    /* embedding: dE[tok] += rows of the input gradient, per token in
+     * ascending row order */
     {
-        hipDeviceptr_t dx = g->dres, order = g->emb_order, seg = g->emb_seg, dE = G_(g, 0);
+        hipDeviceptr_t dx = g->dres[v % R], order = g->emb_order, seg = g->emb_seg, dE = G_(g, 0);
         hipDeviceptr_t seg_tok = dptr(seg, g->emb_nseg + 1);
         i32 nseg = (i32)g->emb_nseg;
         void* args[] = { &dx, &order, &seg, &seg_tok, &nseg, &dE, &D };

@@ -6,13 +6,6 @@
 // reductions everywhere (no atomics), so reruns are bit-identical.
 #include "common.h"
 
-// ---------------------------------------------------------------- fill
-extern "C" __global__ void __launch_bounds__(256) k_fill_zero(float* __restrict__ p, long long n) {
-    long long i = (long long)blockIdx.x * blockDim.x + threadIdx.x;
-    long long stride = (long long)gridDim.x * blockDim.x;
-    for (; i < n; i += stride) p[i] = 0.f;
-}
-
 // ---------------------------------------------------------------- embedding
 // x[n, :] = E[ids[n], :]  (train_kernels.cu:724-730). Bit-exact gather.
 extern "C" __global__ void __launch_bounds__(256)
@@ -99,14 +92,17 @@ k_rmsnorm_fwd(const float* __restrict__ x, const float* __restrict__ w, float* _
     for (int i = lane; i < cols; i += 64) orow[i] = xr[i] * r * w[i];
 }
 
-// dx += w*r*dy - (r^3/cols)*x*S, S = sum(dy*w*x)  (model_ops.c:89-117,
-// train_kernels.cu:552-569).  The weight gradient dy*x*r is reduced over the
-// block's RMS_ROWS rows in row order and written as one partial row per
-// block; k_colsum_final adds the partials in block order.
+// dx = dxin + (w*r*dy - (r^3/cols)*x*S), S = sum(dy*w*x)  (model_ops.c:89-117,
+// train_kernels.cu:552-569: the reference adds into dx in place; here the
+// incoming gradient dxin is a separate buffer, or zero when dxin is null).
+// The weight gradient dy*x*r is reduced over the block's RMS_ROWS rows in
+// row order and written as one partial row per block; k_colsum_final adds
+// the partials in block order.
 #define RMS_ROWS 16
 extern "C" __global__ void __launch_bounds__(256)
 k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const float* __restrict__ rinv,
-              const float* __restrict__ dy, float* __restrict__ dx, float* __restrict__ wpart, int rows, int cols) {
+              const float* __restrict__ dy, const float* __restrict__ dxin, float* __restrict__ dx,
+              float* __restrict__ wpart, int rows, int cols) {
     extern __shared__ float part[];   // [4][cols]
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const int r0 = blockIdx.x * RMS_ROWS;
@@ -129,6 +125,7 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
             if (row >= rows) break;
             const float* xr = x + (long long)row * cols;
             const float* d = dy + (long long)row * cols;
+            const float* gi = dxin + (long long)row * cols;
             float* g = dx + (long long)row * cols;
             f32x4 xv[4], dv[4], gv[4];
             float S = 0.f;
@@ -138,7 +135,7 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
                 const bool ok = q < c4;
                 xv[i] = ok ? *(const f32x4*)(xr + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
                 dv[i] = ok ? *(const f32x4*)(d + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
-                gv[i] = ok ? *(const f32x4*)(g + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
+                gv[i] = ok && dxin ? *(const f32x4*)(gi + 4 * q) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
                 for (int e = 0; e < 4; e++) S += dv[i][e] * wv[i][e] * xv[i][e];
             }
@@ -171,6 +168,7 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
             if (row >= rows) break;
             const float* xr = x + (long long)row * cols;
             const float* d = dy + (long long)row * cols;
+            const float* gi = dxin + (long long)row * cols;
             float* g = dx + (long long)row * cols;
             float r = rinv[row];
             float r3 = r * r * r;
@@ -179,7 +177,7 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
             S = wave_sum(S);
             float c = r3 / (float)cols;
             for (int j = lane; j < cols; j += 64) {
-                g[j] += w[j] * r * d[j] - c * xr[j] * S;
+                g[j] = (dxin ? gi[j] : 0.f) + (w[j] * r * d[j] - c * xr[j] * S);
                 mine[j] += d[j] * xr[j] * r;
             }
         }
