@@ -76,6 +76,11 @@ hipStream_t hip_current_stream(void);
  * work queued so far.  hip_sync and hip_free also wait for the side stream. */
 #define HIP_SIDE_MARKS 8
 void hip_side_begin(void);
+/* hip_side_serial(1): until hip_side_serial(0), in every context of the
+ * process, side sections run on the main stream in the order they are
+ * issued and marks / waits / joins are no-ops -- the same work as one stream
+ * (for checking the overlap).  Call between operations, not inside one. */
+void hip_side_serial(i32 on);
 void hip_side_end(i32 mark);
 void hip_main_wait(i32 mark);
 void hip_side_join(void);

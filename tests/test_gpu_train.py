@@ -196,3 +196,38 @@ def test_adamw(case, trlm, orc):
     want = p.copy(); m = np.zeros_like(p); v = np.zeros_like(p)
     orc.adam_step(want, G, m, v, 1, 3e-4, 0.9, 0.95, 1e-8, 0.1)
     assert int((np.abs(got - want) > 1e-3 * 3e-4 + 1e-6 * np.abs(want)).sum()) == 0
+
+
+def test_overlap_equals_serial_at_config4(trlm, orc):
+    """Config 4 (the 12-layer d=384 model, B=8, T=1024): the backward with its
+    weight-gradient work overlapped on the side stream gives the same loss and
+    gradients, bit for bit, as the same kernels in one stream order -- at the
+    real shape, where the side sections and the main chain run concurrently.
+    Then a rerun with overlap again repeats the first result."""
+    V, D, H, L, F, T, B = 31769, 384, 6, 12, 1024, 1024, 8
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    tokens = orc.random_tokens(40000, V)
+    ids, tgt = orc.sample_batch(tokens, T, B, 2026)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, B, T)
+    _, hip = trlm.libs()
+    try:
+        l1 = np.float32(tr.forward_backward(ids, tgt))
+        g1 = tr.grads()
+        hip.hip_side_serial(1)
+        try:
+            l2 = np.float32(tr.forward_backward(ids, tgt))
+            g2 = tr.grads()
+        finally:
+            hip.hip_side_serial(0)
+        l3 = np.float32(tr.forward_backward(ids, tgt))
+        g3 = tr.grads()
+    finally:
+        tr.destroy()
+        hm.close()
+    assert abs(float(l1) - np.log(V)) < 0.5, l1
+    assert np.isfinite(g1).all()
+    assert l1.view(np.uint32) == l2.view(np.uint32) == l3.view(np.uint32)
+    assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
+    assert np.array_equal(g1.view(np.uint32), g3.view(np.uint32))

@@ -198,8 +198,13 @@ void hip_launch(hipFunction_t f, u32 gx, u32 gy, u32 gz, u32 bx, u32 by, u32 bz,
           "hipModuleLaunchKernel");
 }
 
+static int side_serial;
+
+void hip_side_serial(i32 on) { side_serial = on != 0; }
+
 void hip_side_begin(void) {
     HipCtx* c = current("hip_side_begin");
+    if (side_serial) return;
     if (!c->side) {
         HipSide* s = (HipSide*)calloc(1, sizeof(HipSide));
         check(hipStreamCreateWithFlags(&s->stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
@@ -224,6 +229,7 @@ static void check_mark(i32 mark, const char* what) {
 void hip_side_end(i32 mark) {
     HipCtx* c = current("hip_side_end");
     check_mark(mark, "hip_side_end");
+    if (side_serial) return;
     if (!c->side || !c->side->active) {
         fprintf(stderr, "[HIP ERROR] hip_side_end without hip_side_begin\n");
         fatal_exit();
@@ -235,7 +241,7 @@ void hip_side_end(i32 mark) {
 void hip_main_wait(i32 mark) {
     HipCtx* c = current("hip_main_wait");
     check_mark(mark, "hip_main_wait");
-    if (!c->side) return;   /* nothing was ever queued on the side stream */
+    if (side_serial || !c->side) return;   /* no side stream, or nothing queued on it */
     check(hipStreamWaitEvent(c->stream, c->side->mark[mark], 0), "hipStreamWaitEvent");
 }
 

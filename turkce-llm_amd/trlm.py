@@ -196,6 +196,7 @@ def _bind(host, hip):
     _sig(hip, "hip_init", HipCtx, [AP, C.c_char_p])
     _sig(hip, "hip_device_count", C.c_int32, [])
     _sig(hip, "hip_shutdown", None, [HP])
+    _sig(hip, "hip_side_serial", None, [C.c_int32])
     _sig(hip, "hip_set_current", None, [HP])
     _sig(hip, "hip_get_kernel", C.c_void_p, [HP, C.c_char_p])
     _sig(hip, "hip_alloc", C.c_void_p, [C.c_uint64])
