@@ -589,28 +589,42 @@ __device__ void flash_bwd_dq_ds(const AttnParams& p) {
     const int nkv = qb + 1;
     const int niter = (nkv + 1) / 2;
     const float* KT = lds + part * HD * ATT_LDT;
+    // this lane's query qq = l%32 of group grp sits in rows r(qq) of the
+    // (key group, grp) sub-blocks, in lane half (qq/4)&1
+    const int qq = lane & 31;
+    const int ds_off = grp * 1024 + ((qq >> 3) * 4 + (qq & 3)) * 64 + ((qq >> 2) & 1) * 32 + 4 * half;
+    // Software pipeline: the K tiles of stage it + 1 and this wave's dS block
+    // of that stage are loaded while stage it's MFMAs run.
+    AttTileT<HD> tk[2];
+    f32x4 sv[8];
+    tk[0].load(qkv, p.ldq, 0, p.T, kcol);
+    tk[1].load(qkv, p.ldq, 64, p.T, kcol);
+    if (part < nkv) {
+        const float* row = att_ds_block(p, bh, qb, part) + ds_off;
+#pragma unroll
+        for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
+    }
     for (int it = 0; it < niter; it++) {
         // K of the stage's two key blocks, transposed ([HD][ATT_LDT]); rows
         // past the end are stored as zeros
-#pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            const int kbp = 2 * it + pp;
-            AttTileT<HD> tk;
-            tk.load(qkv, p.ldq, kbp * 64, p.T, kcol);
-            if (pp == 0) __syncthreads();
-            tk.store(lds + pp * HD * ATT_LDT, kbp * 64, p.T);
-        }
+        if (it > 0) __syncthreads();
+        tk[0].store(lds, 2 * it * 64, p.T);
+        tk[1].store(lds + HD * ATT_LDT, (2 * it + 1) * 64, p.T);
         __syncthreads();
         const int kb = 2 * it + part;
-        if (kb >= nkv) continue;
-        // this lane's query qq = l%32 of group grp sits in rows r(qq) of the
-        // (key group, grp) sub-blocks, in lane half (qq/4)&1
-        const int qq = lane & 31;
-        const float* row = att_ds_block(p, bh, qb, kb) + grp * 1024 + ((qq >> 3) * 4 + (qq & 3)) * 64 +
-                           ((qq >> 2) & 1) * 32 + 4 * half;
-        f32x4 sv[8];
+        f32x4 cur[8];
 #pragma unroll
-        for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
+        for (int c = 0; c < 8; c++) cur[c] = sv[c];
+        if (it + 1 < niter) {
+            tk[0].load(qkv, p.ldq, (2 * it + 2) * 64, p.T, kcol);
+            tk[1].load(qkv, p.ldq, (2 * it + 3) * 64, p.T, kcol);
+            if (kb + 2 < nkv) {
+                const float* row = att_ds_block(p, bh, qb, kb + 2) + ds_off;
+#pragma unroll
+                for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
+            }
+        }
+        if (kb >= nkv) continue;
 #pragma unroll
         for (int c = 0; c < 8; c++) {
 #pragma unroll
@@ -619,7 +633,7 @@ __device__ void flash_bwd_dq_ds(const AttnParams& p) {
                 const f32x4 ka = dc < HD ? *(const f32x4*)(KT + dc * ATT_LDT + 8 * c + 4 * half)
                                          : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-                for (int t = 0; t < 4; t++) acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], sv[c][t], acc[d], 0, 0, 0);
+                for (int t = 0; t < 4; t++) acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], cur[c][t], acc[d], 0, 0, 0);
             }
         }
     }
@@ -675,7 +689,7 @@ __device__ void attn_dvec(const AttnParams& p) {
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dkv_hd##HD(AttnParams p) { \
         flash_bwd_dkv<HD>(p);                                                                             \
     }                                                                                                     \
-    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4))) k_attn_bwd_dq_hd##HD(AttnParams p) { \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) k_attn_bwd_dq_hd##HD(AttnParams p) { \
         flash_bwd_dq_ds<HD>(p);                                                                           \
     }                                                                                                     \
     extern "C" __global__ void __launch_bounds__(256) k_attn_dvec_hd##HD(AttnParams p) { attn_dvec<HD>(p); }
