@@ -19,6 +19,11 @@ with HIP events on the library's stream.
 cpu_baseline: the reference's own CPU matmul (tensor_matmul2d, built from
 /root/reference into oracle/_ref) on a bounded sample of the sweep; falls
 back to the oracle restatement when oracle/_ref was not built.
+cpu_train: the reference's CPU training step on the host cores (one thread
+per sequence running lm_forward + backward, the gradient average, then
+adam_step_parallel, as training/data_parallel.c and training/adam.c run it)
+on a bounded sample (the real 12-layer model, one T=16 sequence per
+thread), as tokens/s beside the GPU's config-4 rate.
 """
 import argparse
 import ctypes as C
@@ -302,6 +307,37 @@ def cpu_baseline(seconds_target=10.0):
                 else "the oracle's reference-order matmul", dt)}
 
 
+def cpu_train_baseline(T=16):
+    """The reference's CPU training step (oracle/_ref; the oracle's port
+    otherwise) on the real architecture, one sequence of T tokens per host
+    thread, timed once."""
+    import oracle
+    threads = max(1, min(16, os.cpu_count() or 1))
+    model = oracle.Model(V, D, H, L, F)
+    tok = oracle.random_tokens(4 * threads * T + T + 2, V)
+    ids, tgt = oracle.sample_batch(tok, T, threads, 2026)
+    if oracle.reference_available():
+        ref = oracle.Reference()
+        params = ref.lm_init(model)
+        grads = np.zeros(model.total, np.float32)
+        scratch = np.zeros(model.total * threads, np.float32)
+        run = lambda b: ref.h.refh_time_train_step(C.byref(model.cfg), params, ids, tgt, b, T, model.total,
+                                                   grads, scratch, threads)
+        kind = "reference"
+    else:
+        params = model.init(1337, 1)
+
+        def run(b):
+            t0 = time.perf_counter()
+            model.forward_backward(params, ids[:b * T], tgt[:b * T], b, T)
+            return time.perf_counter() - t0
+        kind = "port"
+    dt = run(threads)
+    return {"tokens_per_s": threads * T / dt, "threads": threads, "kind": kind,
+            "sample": "%d sequences x T=%d of the 12-layer d=384 model, one per thread: forward, backward, "
+                      "gradient average, adam_step_parallel; %.1f s" % (threads, T, dt)}
+
+
 def summarize_profile(path):
     """Print per-kernel statistics from a rocprofv3 run (--kernel-trace
     --output-format csv): one line per (kernel, grid) so that the LM-head
@@ -547,6 +583,13 @@ def main():
         line["cpu_baseline"] = {"value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
                                 "sample": cb["sample"]}
         line["gpu_vs_cpu_gemm"] = round(value / cb["value"], 1)
+        if not args.no_model:
+            log("cpu baseline: reference training step on the host cores")
+            ct = cpu_train_baseline()
+            line["cpu_train"] = {"tokens_per_s": round(ct["tokens_per_s"], 2), "threads": ct["threads"],
+                                 "kind": ct["kind"], "sample": ct["sample"]}
+            if "train_tokens_per_s" in line:
+                line["gpu_vs_cpu_train"] = round(line["train_tokens_per_s"] / ct["tokens_per_s"], 1)
     print(json.dumps(line), flush=True)
 
 
