@@ -22,7 +22,7 @@ back to the oracle restatement when oracle/_ref was not built.
 cpu_train: the reference's CPU training step on the host cores (one thread
 per sequence running lm_forward + backward, the gradient average, then
 adam_step_parallel, as training/data_parallel.c and training/adam.c run it)
-on a bounded sample (the real 12-layer model, one T=16 sequence per
+on a bounded sample (the real 12-layer model, one T=32 sequence per
 thread), as tokens/s beside the GPU's config-4 rate.
 """
 import argparse
@@ -307,7 +307,7 @@ def cpu_baseline(seconds_target=10.0):
                 else "the oracle's reference-order matmul", dt)}
 
 
-def cpu_train_baseline(T=16):
+def cpu_train_baseline(T=32):
     """The reference's CPU training step (oracle/_ref; the oracle's port
     otherwise) on the real architecture, one sequence of T tokens per host
     thread, timed once."""
