@@ -59,10 +59,12 @@ struct GemmParams {
 // RoPE of four consecutive output columns n..n+3 of row `row` (model/rope.c:
 // 20-40): pairs (2k, 2k+1) of a head of rope_hd columns rotated by
 // (cos, sin)[t = row % rope_T, k]; the tables are [rope_T][rope_hd/2].
+// n is a multiple of 4, so k is even and each table pair is one 8-byte load.
 __device__ __forceinline__ void rope4(const GemmParams& p, int row, int n, f32x4& v) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
     const int t = row % p.rope_T, k = (n % p.rope_hd) >> 1, hh = p.rope_hd >> 1;
-    const float c0 = p.rope_cos[t * hh + k], c1 = p.rope_cos[t * hh + k + 1];
-    const float s0 = p.rope_sin[t * hh + k], s1 = p.rope_sin[t * hh + k + 1];
+    const f32x2 cc = *(const f32x2*)(p.rope_cos + t * hh + k), ss = *(const f32x2*)(p.rope_sin + t * hh + k);
+    const float c0 = cc[0], c1 = cc[1], s0 = ss[0], s1 = ss[1];
     const f32x4 a = v;
     v[0] = a[0] * c0 - a[1] * s0;
     v[1] = a[0] * s0 + a[1] * c0;
