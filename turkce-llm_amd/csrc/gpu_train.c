@@ -83,13 +83,11 @@ static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
 
 #define RMS_ROWS 16u
 
-/* dx += RMSNorm backward; dw = sum over rows of dy*x*r  (gpu_train.c:132-140) */
-/* The weight gradient's final column sum runs on the side stream (marks 5
- * and 6), off the dX chain; the partial buffers alternate, and the main
- * stream waits for a buffer's previous sum before refilling it. */
-/* RMSNorm backward on the current stream: dx = dxin (zero when dxin is 0) +
- * the norm's input gradient, and the weight gradient's per-block partials
- * into part (rows in order; colsum_partials adds them up). */
+/* RMSNorm backward (gpu_train.c:132-140) on the current stream: dx = dxin
+ * (zero when dxin is 0) + the norm's input gradient, and the weight
+ * gradient dw = sum over rows of dy*x*r as per-block partials into part
+ * (rows in order; colsum_partials adds them up, on the side stream in the
+ * backward). */
 static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t rinv, hipDeviceptr_t dy,
                         hipDeviceptr_t dxin, hipDeviceptr_t dx, hipDeviceptr_t part) {
     i32 rows = (i32)g->N, cols = (i32)g->D;
