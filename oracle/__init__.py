@@ -314,6 +314,7 @@ class Reference:
         h.refh_adam_step.argtypes = [cfgp, f32p, f32p, f32p, f32p, C.c_uint64, C.c_float,
                                      C.c_float, C.c_float, C.c_float]
         h.refh_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
+        h.refh_sample_batch.argtypes = [u32p, C.c_uint64, C.c_uint32, C.c_uint32, C.c_uint64, u32p, u32p]
         h.refh_lr_schedule.argtypes = [C.c_uint64, C.c_uint32, C.c_uint64, C.c_uint64, C.c_float, C.c_float, f32p]
         h.refh_time_train_step.restype = C.c_double
         h.refh_time_train_step.argtypes = [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32,
@@ -375,6 +376,14 @@ class Reference:
         ok = self.h.refh_checkpoint_load(C.byref(c), path.encode(), p, m.ctypes.data if want_opt else None,
                                          v.ctypes.data if want_opt else None, C.byref(t), int(want_opt))
         return (p, m, v, t.value) if ok else None
+
+    def sample_batch(self, tokens, T, B, seed_base):
+        """gpu_trainer_sample_batch of the reference (model/gpu_train.c:296-307)."""
+        tokens = np.ascontiguousarray(tokens, np.uint32)
+        ids = np.zeros(B * T, np.uint32)
+        tgt = np.zeros(B * T, np.uint32)
+        self.h.refh_sample_batch(tokens, len(tokens), T, B, seed_base, ids, tgt)
+        return ids, tgt
 
     def lr_schedule(self, first, n, warmup, total, peak, min_lr):
         out = np.zeros(n, np.float32)

@@ -7,7 +7,9 @@
  *
  * The reference library is opened with RTLD_LAZY: its model files reference
  * the GPU matmul entry points (model/gpu_ops.h), which are not built here
- * and are never called on this path (use_gpu_layers = use_gpu_output = 0).
+ * and are never called on this path (use_gpu_layers = use_gpu_output = 0);
+ * likewise model/gpu_train.c is in the library only for its host-side batch
+ * sampler, and its cuda_* calls are never reached.
  *
  * The per-sequence threading and gradient averaging below restate
  * data_parallel_step (training/data_parallel.c:156-199), whose own worker
@@ -58,6 +60,7 @@ static struct {
     bool32 (*checkpoint_save)(const char*, Node**, u32, const AdamOptimizer*);
     bool32 (*checkpoint_load)(Allocator*, const char*, Node**, u32, AdamOptimizer*);
     f32 (*lr_warmup_cosine)(u64, u64, u64, f32, f32);
+    void (*gpu_trainer_sample_batch)(const u32*, u64, u32, u32, u64, u32*, u32*);
     int ok;
 } R;
 
@@ -76,6 +79,7 @@ int refh_open(const char* lib_path) {
     LOAD(m_powf); LOAD(m_expf); LOAD(m_logf); LOAD(m_sqrtf); LOAD(m_sinf); LOAD(m_cosf);
     LOAD(checkpoint_save); LOAD(checkpoint_load);
     LOAD(lr_warmup_cosine);
+    LOAD(gpu_trainer_sample_batch);
     R.ok = 1;
     return 0;
 }
@@ -102,6 +106,11 @@ double refh_m(int which, double x, double y) {
 /* lr_warmup_cosine (training/lr_schedule.c) for steps first..first+n-1. */
 void refh_lr_schedule(u64 first, u32 n, u64 warmup, u64 total, f32 peak, f32 min_lr, f32* out) {
     for (u32 i = 0; i < n; i++) out[i] = R.lr_warmup_cosine(first + i, warmup, total, peak, min_lr);
+}
+
+/* The reference's batch sampler (model/gpu_train.c:296-307), host code only. */
+void refh_sample_batch(const u32* tokens, u64 num_tokens, u32 T, u32 B, u64 seed_base, u32* ids, u32* tgt) {
+    R.gpu_trainer_sample_batch(tokens, num_tokens, T, B, seed_base, ids, tgt);
 }
 
 void refh_pcg_u32(u64 sa, u64 sb, u32 n, u32* out) {

@@ -22,8 +22,12 @@
  *                           central-difference gradient check on a tiny model.
  *   or_adam_step            oracle/_ref adam_step bit-equality; closed form
  *                           first step ~ lr*sign(g); AdamW(wd=0) == Adam.
- *   or_sample_batch         oracle/_ref-free: integer identity with the
- *                           data_parallel window formula and PCG KAT.
+ *   or_sample_batch         bit-equality with the reference's own
+ *                           gpu_trainer_sample_batch (model/gpu_train.c,
+ *                           compiled into oracle/_ref) and its frozen
+ *                           windows in tests/golden/.
+ *   or_argmax               numpy's first maximum on NaN-free rows and the
+ *                           explicit NaN / -inf cases of its rule.
  */
 #ifndef TRLM_ORACLE_H
 #define TRLM_ORACLE_H
@@ -89,6 +93,9 @@ float or_forward_backward(const OrCfg* c, const float* params, const uint32_t* i
 void or_adam_step(float* p, const float* g, float* m, float* v, uint64_t n, uint64_t t,
                   float lr, float b1, float b2, float eps, float wd, float grad_scale);
 
+/* Greedy pick: the reference's max scan (generate.c:57-58) -- best starts at
+ * index 0 and moves only to a strictly greater value, so ties keep the first
+ * index, a NaN at index 0 keeps 0 and other NaNs are never picked. */
 uint32_t or_argmax(const float* row, uint32_t n);
 /* sample_next (training/generate.c:57-73) on one row of logits; scratch [n]. */
 uint32_t or_sample_next(const float* logits, uint32_t n, float temperature, OrPcg* rng, float* scratch);

@@ -8,9 +8,12 @@ Outputs (data only: inputs and the reference's outputs):
                     token ids/targets, logits, loss, averaged gradients, and
                     one Adam step (the first case of test_gpu_train.c)
   ref_scalars.json  scalar maths and PCG outputs at fixed points, SHA-256 of
-                    the real model's lm_init bits and of RoPE tables, and the
+                    the real model's lm_init bits and of RoPE tables, the
                     real-scale (V31769 D384 H6 L12 F1024 T128 B4) loss with
-                    per-tensor gradient sums
+                    per-tensor gradient sums, and SHA-256 of the batches the
+                    reference's gpu_trainer_sample_batch (model/gpu_train.c:
+                    296-307) draws for SAMPLE_CASES
+Every token window below comes from the reference's own sampler.
 """
 import hashlib
 import json
@@ -35,6 +38,21 @@ MATH_POINTS = {
 POW_POINTS = [(2.0, 10.0), (2.0, 0.5), (-2.0, 3.0), (0.9, 7.0), (0.999, 3.0), (10000.0, -0.03125)]
 F32_POINTS = {"sqrtf": [2.0, 64.0, 1e-5, 0.3], "expf": [1.0, -3.25, -60.0], "logf": [31769.0, 1.5],
               "sinf": [0.5235988, 1023.0], "cosf": [0.5235988, 1023.0]}
+# (num_tokens, vocab, token seed a, token seed b, T, B, seed_base): the
+# fixtures' own windows, the config-4 stream at seeds 2026 + step, and edges
+# (max_start = 0 and 1, seed_base * 1000003 wrapping past 2^64).
+SAMPLE_CASES = [
+    (4000, 50, 4242, 7, 12, 5, 2026),
+    (200000, 31769, 4242, 7, 128, 4, 2026),
+    (200000, 31769, 4242, 7, 1024, 8, 2026),
+    (200000, 31769, 4242, 7, 1024, 8, 2027),
+    (200000, 31769, 4242, 7, 1024, 8, 2028),
+    (5000, 300, 1, 2, 50, 6, 9),
+    (13, 50, 3, 3, 12, 3, 7),
+    (14, 50, 3, 3, 12, 9, 8),
+    (70000, 1000, 5, 6, 333, 17, (1 << 63) + 12345),
+]
+
 WHICH = {"sqrt": 0, "exp": 1, "log": 2, "pow": 3, "sin": 4, "cos": 5,
          "sqrtf": 10, "expf": 11, "logf": 12, "powf": 13, "sinf": 14, "cosf": 15}
 
@@ -78,12 +96,19 @@ def main():
     out["real_init_sha256"] = sha(p)
     out["real_num_params"] = int(real.total)
     toks = oracle.random_tokens(200000, 31769)
-    ids, tgt = oracle.sample_batch(toks, 128, 4, 2026)
+    ids, tgt = ref.sample_batch(toks, 128, 4, 2026)
     out["real_ids_sha256"] = sha(ids)
     loss, grads = ref.forward_backward(real, p, ids, tgt, 4, 128)
     out["real_loss_hex"] = float(loss).hex()
     out["real_grad_tensor_sums"] = [float(x.astype(np.float64).sum()).hex() for x in real.split(grads)]
     out["real_grad_sha256"] = sha(grads)
+    # the reference's batch sampler
+    sb = []
+    for n, V, sa, sbb, T, B, seed in SAMPLE_CASES:
+        toks = oracle.random_tokens(n, V, sa, sbb)
+        i, t = ref.sample_batch(toks, T, B, seed)
+        sb.append([n, V, sa, sbb, T, B, seed, sha(i), sha(t)])
+    out["sample_batch"] = sb
     with open(os.path.join(HERE, "ref_scalars.json"), "w") as fh:
         json.dump(out, fh, indent=1, sort_keys=True)
 
@@ -91,7 +116,7 @@ def main():
     small = oracle.Model(50, 32, 2, 2, 48)
     ps = ref.lm_init(small, 1337, 1)
     toks = oracle.random_tokens(4000, 50)
-    ids, tgt = oracle.sample_batch(toks, 12, 5, 2026)
+    ids, tgt = ref.sample_batch(toks, 12, 5, 2026)
     logits = ref.forward_logits(small, ps, ids, 5, 12)
     loss, grads = ref.forward_backward(small, ps, ids, tgt, 5, 12)
     pa, ma, va = ps.copy(), np.zeros_like(ps), np.zeros_like(ps)

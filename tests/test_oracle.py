@@ -229,15 +229,65 @@ def test_adam_closed_form(orc):
     assert np.allclose(q3, p * (1 - 3e-4 * 0.1), rtol=1e-6)
 
 
-def test_sample_batch_windows(orc):
-    toks = orc.random_tokens(5000, 300, 1, 2)
-    ids, tgt = orc.sample_batch(toks, 50, 6, 9)
-    ids, tgt = ids.reshape(6, 50), tgt.reshape(6, 50)
-    assert np.array_equal(ids[:, 1:], tgt[:, :-1])
-    for w in range(6):
-        r = orc.pcg_stream(9 * 1000003 + w, 99 + w)
-        start = orc.lib().or_pcg_range_i64(C.byref(r), 0, 5000 - 50 - 1)
-        assert np.array_equal(ids[w], toks[start:start + 50])
+def test_sample_batch_matches_reference_fixture(orc, scalars):
+    """or_sample_batch against the batches the reference's own
+    gpu_trainer_sample_batch (model/gpu_train.c:296-307) drew, frozen by
+    make_golden.py: the fixtures' windows, the config-4 stream at seeds
+    2026..2028, max_start 0 and 1, and seed_base * 1000003 wrapping."""
+    assert len(scalars["sample_batch"]) >= 9
+    for n, V, sa, sb, T, B, seed, want_ids, want_tgt in scalars["sample_batch"]:
+        toks = orc.random_tokens(n, V, sa, sb)
+        ids, tgt = orc.sample_batch(toks, T, B, seed)
+        assert sha(ids) == want_ids, (n, T, B, seed)
+        assert sha(tgt) == want_tgt, (n, T, B, seed)
+        ids, tgt = ids.reshape(B, T), tgt.reshape(B, T)
+        assert np.array_equal(ids[:, 1:], tgt[:, :-1])
+
+
+@pytest.mark.skipif(not __import__("oracle").reference_available(), reason="oracle/_ref not built")
+def test_sample_batch_matches_compiled_reference(orc):
+    """or_sample_batch bit for bit against the reference's
+    gpu_trainer_sample_batch compiled into oracle/_ref, on random shapes and
+    seeds (including seeds past 2^63)."""
+    ref = orc.Reference()
+    rng = np.random.default_rng(5)
+    for case in range(40):
+        T = int(rng.integers(1, 300))
+        n = T + 1 + int(rng.integers(0, 5000))
+        B = int(rng.integers(1, 12))
+        seed = int(rng.integers(0, 2**64, dtype=np.uint64))
+        toks = rng.integers(0, 2**32, n, dtype=np.uint64).astype(np.uint32)
+        got = orc.sample_batch(toks, T, B, seed)
+        want = ref.sample_batch(toks, T, B, seed)
+        assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), (T, n, B, seed)
+
+
+def test_argmax_rule(orc):
+    """or_argmax follows the reference's max scan (generate.c:57-58: best
+    from index 0, moved only by a strictly greater value): on NaN-free rows
+    it is numpy's first maximum; a NaN at index 0 keeps 0; NaNs elsewhere
+    are never picked; a row with nothing above -inf gives 0."""
+    L = orc.lib()
+    rng = np.random.default_rng(3)
+    for n in (1, 2, 7, 64, 1000, 31769):
+        for _ in range(5):
+            row = rng.standard_normal(n).astype(np.float32)
+            if n > 3:
+                row[rng.integers(0, n, 3)] = row.max()     # ties: first one wins
+            assert L.or_argmax(row, n) == int(np.argmax(row))
+    nan, inf = np.float32("nan"), np.float32("inf")
+    cases = [
+        ([nan, 1.0, 2.0], 0),
+        ([nan, nan, nan], 0),
+        ([1.0, nan, 3.0, nan], 2),
+        ([-inf, -inf, -inf], 0),
+        ([-inf, nan, -inf], 0),
+        ([-inf, nan, -5.0], 2),
+        ([2.0, nan, 2.0], 0),
+    ]
+    for row, want in cases:
+        a = np.array(row, np.float32)
+        assert L.or_argmax(a, len(a)) == want, row
 
 
 def test_sample_next_closed_forms(orc):
