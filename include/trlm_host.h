@@ -17,9 +17,29 @@
  * calls (allocation, tensor views, RoPE tables, PCG, scalar maths).  In a
  * drop-in build they resolve to the reference's own objects; standalone they
  * come from libtrlm_host.so (turkce-llm_amd/csrc/host/trlm_host.c).
+ *
+ * Installed in the reference tree (this header beside model/lm_model.h, as
+ * the drop-in puts it), the definitions come from the reference's own
+ * headers instead, so the reference's callers, which include those headers
+ * too, see each type defined once.  TRLM_STANDALONE_TYPES forces the
+ * definitions below.
  */
 #ifndef TRLM_HOST_H
 #define TRLM_HOST_H
+
+#if !defined(TRLM_STANDALONE_TYPES) && __has_include("lm_model.h") && __has_include("../runtime/types.h") && \
+    __has_include("../training/adam.h")
+#define TRLM_HOST_FROM_REFERENCE 1
+#include "../runtime/types.h"
+#include "../runtime/memory.h"
+#include "../runtime/prng.h"
+#include "../runtime/mathlib.h"
+#include "../tensor/tensor.h"
+#include "../autograd/node.h"
+#include "lm_model.h"
+#include "rope.h"
+#include "../training/adam.h"
+#else
 
 typedef unsigned char      u8;
 typedef unsigned short     u16;
@@ -172,4 +192,5 @@ void rope_build_tables(Tensor* cos_out, Tensor* sin_out, u64 seq_len, u64 head_d
 }
 #endif
 
+#endif /* types from the reference's headers */
 #endif /* TRLM_HOST_H */

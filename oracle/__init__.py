@@ -116,6 +116,11 @@ class Model:
         out.append((D,))
         return out
 
+    def names(self):
+        """Per-tensor names in lm_collect_params order (embed, l<i>.<kind>, final_norm)."""
+        kinds = ["attn_norm", "w_qkv", "b_qkv", "wo", "bo", "ffn_norm", "w_gate_up", "b_gate_up", "w_down", "b_down"]
+        return ["embed"] + ["l%d.%s" % (l, k) for l in range(self.L) for k in kinds] + ["final_norm"]
+
     def split(self, flat):
         return [flat[int(o):int(o) + int(n)].reshape(s)
                 for o, n, s in zip(self.offsets, self.numels, self.shapes())]

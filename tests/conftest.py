@@ -26,6 +26,18 @@ def load_trlm():
     return mod
 
 
+def parity_report(name, rows, header="tensor  max|got-want|  max|want|  ratio"):
+    """Per-tensor max-abs errors of a parity test: printed, and written to
+    $TRLM_PARITY_REPORT/<name>.txt when that directory is set."""
+    lines = [header] + ["%-16s %.3e  %.3e  %.2e" % (n, e, m, e / (m + 1e-30)) for n, e, m in rows]
+    print("\n".join(["[%s]" % name] + lines))
+    out = os.environ.get("TRLM_PARITY_REPORT")
+    if out:
+        os.makedirs(out, exist_ok=True)
+        with open(os.path.join(out, name + ".txt"), "w") as fh:
+            fh.write("\n".join(lines) + "\n")
+
+
 @pytest.fixture(scope="session")
 def trlm():
     return load_trlm()

@@ -2,7 +2,8 @@
 path, compiled from /root/reference into oracle/_ref (oracle/Makefile).
 
 Run in the build container (where /root/reference exists):
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py           (a few minutes)
+    python tests/golden/make_golden.py t1024     (ref_real_t1024.npz, ~15 min)
 Outputs (data only: inputs and the reference's outputs):
   ref_small.npz     off-grid model V50 D32 H2 L2 F48 T12 B5: lm_init params,
                     token ids/targets, logits, loss, averaged gradients, and
@@ -13,6 +14,11 @@ Outputs (data only: inputs and the reference's outputs):
                     per-tensor gradient sums, and SHA-256 of the batches the
                     reference's gpu_trainer_sample_batch (model/gpu_train.c:
                     296-307) draws for SAMPLE_CASES
+  ref_real_t1024.npz  the real model (V31769 D384 H6 L12 F1024, lm_init
+                    pcg_seed(1337,1)) at T=1024 B=2 (windows of the 200,000
+                    token stream, seed 2026): loss, logits rows (sequence,
+                    position) in LOGIT_ROWS, and per gradient tensor max|g|,
+                    sum g (f64), sum |g| (f64) and GRAD_SAMPLES seeded entries
 Every token window below comes from the reference's own sampler.
 """
 import hashlib
@@ -59,6 +65,40 @@ WHICH = {"sqrt": 0, "exp": 1, "log": 2, "pow": 3, "sin": 4, "cos": 5,
 
 def sha(a):
     return hashlib.sha256(np.ascontiguousarray(a).view(np.uint8)).hexdigest()
+
+
+LOGIT_ROWS = [(0, 0), (0, 1), (0, 1023), (1, 511), (1, 1023)]
+GRAD_SAMPLES = 256
+
+
+def t1024():
+    oracle.build(with_ref=True)
+    ref = oracle.Reference()
+    real = oracle.Model(31769, 384, 6, 12, 1024)
+    p = ref.lm_init(real, 1337, 1)
+    toks = oracle.random_tokens(200000, 31769)
+    T, B = 1024, 2
+    ids, tgt = ref.sample_batch(toks, T, B, 2026)
+    loss, grads = ref.forward_backward(real, p, ids, tgt, B, T, nthreads=B)
+    logits = ref.forward_logits(real, p, ids, B, T, nthreads=B).reshape(B, T, -1)
+    rows = np.stack([logits[b, t] for b, t in LOGIT_ROWS])
+    rng = np.random.default_rng(1024)
+    gmax, gsum, gabs, gidx, gval = [], [], [], [], []
+    for g in real.split(grads):
+        g = g.ravel()
+        gmax.append(np.abs(g).max())
+        gsum.append(g.astype(np.float64).sum())
+        gabs.append(np.abs(g).astype(np.float64).sum())
+        idx = np.sort(rng.choice(g.size, min(GRAD_SAMPLES, g.size), replace=False))
+        idx = np.pad(idx, (0, GRAD_SAMPLES - idx.size), constant_values=idx[-1])
+        gidx.append(idx)
+        gval.append(g[idx])
+    np.savez_compressed(os.path.join(HERE, "ref_real_t1024.npz"), ids=ids, tgt=tgt, loss=np.float32(loss),
+                        logit_rows=np.array(LOGIT_ROWS, np.int32), logits=rows,
+                        grad_max=np.array(gmax, np.float32), grad_sum=np.array(gsum), grad_abs=np.array(gabs),
+                        grad_idx=np.array(gidx, np.int64), grad_val=np.array(gval, np.float32),
+                        params_sha256=np.array(sha(p)))
+    print("wrote ref_real_t1024.npz: loss", float(loss))
 
 
 def main():
@@ -127,4 +167,7 @@ def main():
 
 
 if __name__ == "__main__":
-    main()
+    if len(sys.argv) > 1 and sys.argv[1] == "t1024":
+        t1024()
+    else:
+        main()

@@ -7,7 +7,14 @@
     reference's own gpu_train.c / gpu_ops.c use (so the reference's objects
     can provide them) plus libc / HIP runtime;
   - the gfx950 code object holds every kernel the host code looks up;
-  - the Python structure mirror matches the C compiler's layout;
+  - the Python structure mirror matches the C compiler's layout, and
+    trlm_host.h's host types match the reference's own headers (sizeof and
+    every field offset, compiled from /root/reference when present);
+  - the drop-in binding is real: oracle/dropin.sh compiles every program of
+    the reference (all but tests/test_cuda.c) from its own sources against
+    include/ installed as model/gpu_train.h, model/gpu_ops.h, ... and links
+    it with libtrlm_hip.so instead of the CUDA objects (when
+    /root/reference is present);
   - the host-side logic of the path is bit-identical to the oracle: PCG,
     scalar maths feeding RoPE and Adam, RoPE tables, batch sampling.
 No GPU call is made here (HIP calls without a device would end the process).
@@ -200,3 +207,80 @@ def test_gemm_plan_is_a_pure_function_of_the_shape(trlm):
     # large tile and needs no split
     name = hip.trlm_gemm_plan(0, 1, 8192, 31769, 384, 1, C.byref(sp)).decode()
     assert name == "k_gemm_nt_128x128" and sp.value == 1
+
+
+REF = "/root/reference"
+LAYOUT_PROBE = r"""
+#include <stddef.h>
+#include <stdio.h>
+%s
+#define S(T) printf(#T " %%zu\n", sizeof(T))
+#define O(T, m) printf(#T "." #m " %%zu\n", offsetof(T, m))
+int main(void) {
+    S(Arena); S(Allocator); S(Tensor); S(Node); S(PCGState); S(AttentionWeights); S(FeedForwardWeights);
+    S(BlockWeights); S(LMModel); S(AdamOptimizer);
+    O(Arena, reserved); O(Arena, committed); O(Arena, used);
+    O(Allocator, free_list); O(Allocator, last_phys);
+    O(Tensor, shape); O(Tensor, strides); O(Tensor, ndim); O(Tensor, numel); O(Tensor, owns_data);
+    O(Node, grad); O(Node, requires_grad); O(Node, parents); O(Node, num_parents); O(Node, backward_fn);
+    O(Node, visited); O(Node, aux_dim0); O(Node, aux_dim1); O(Node, aux_scalar); O(Node, aux_ptr);
+    O(PCGState, inc); O(PCGState, has_cached_gaussian); O(PCGState, cached_gaussian);
+    O(AttentionWeights, b_qkv); O(AttentionWeights, wo); O(AttentionWeights, bo);
+    O(FeedForwardWeights, b_gate_up); O(FeedForwardWeights, w_down); O(FeedForwardWeights, b_down);
+    O(BlockWeights, attn); O(BlockWeights, ffn_norm_w); O(BlockWeights, ffn);
+    O(LMModel, blocks); O(LMModel, final_norm_w); O(LMModel, num_layers); O(LMModel, num_heads);
+    O(LMModel, d_model); O(LMModel, vocab_size); O(LMModel, eps);
+    O(AdamOptimizer, m); O(AdamOptimizer, v); O(AdamOptimizer, num_params); O(AdamOptimizer, t);
+    O(AdamOptimizer, lr); O(AdamOptimizer, beta1); O(AdamOptimizer, beta2); O(AdamOptimizer, eps);
+    printf("LM_MAX_LAYERS %%d\n", (int)LM_MAX_LAYERS);
+    return 0;
+}
+"""
+
+
+def _probe(tmp_path, name, includes, flags):
+    src = tmp_path / (name + ".c")
+    src.write_text(LAYOUT_PROBE % includes)
+    exe = tmp_path / name
+    subprocess.run(["gcc", "-std=c11", "-D_DEFAULT_SOURCE"] + flags + [str(src), "-o", str(exe)], check=True)
+    return subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout
+
+
+@pytest.mark.skipif(not os.path.isdir(REF), reason="reference tree not present")
+def test_host_types_match_reference_headers(tmp_path):
+    """sizeof and every field offset of the host types in trlm_host.h equal
+    the reference's own definitions (runtime/types.h, runtime/memory.h,
+    runtime/prng.h, tensor/tensor.h, autograd/node.h, model/*.h,
+    training/adam.h), compiled by the same compiler."""
+    ref_inc = "\n".join('#include "%s"' % h for h in (
+        "runtime/types.h", "runtime/memory.h", "runtime/prng.h", "tensor/tensor.h", "autograd/node.h",
+        "model/lm_model.h", "training/adam.h"))
+    want = _probe(tmp_path, "ref_layout", ref_inc, ["-I" + REF])
+    got = _probe(tmp_path, "our_layout", '#include "trlm_host.h"', ["-I" + INC])
+    assert got == want
+    assert len(got.splitlines()) >= 50
+
+
+@pytest.mark.skipif(not os.path.isdir(REF), reason="reference tree not present")
+def test_reference_programs_link_against_the_library(trlm):
+    """oracle/dropin.sh: the reference's own programs, compiled against
+    include/ as model/gpu_train.h, model/gpu_ops.h (+ hip_backend.h,
+    trlm_host.h, trlm_ext.h), link with libtrlm_hip.so and need no CUDA
+    library.  Among them the callers SURVEY names: train_lm_gpu, generate,
+    chat, train_lm, train_faz4/5, data_parallel's tests, test_gpu_train and
+    test_gpu_ops."""
+    trlm.libs()
+    r = subprocess.run([os.path.join(ROOT, "oracle", "dropin.sh"), REF], capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr[-3000:]
+    out = os.path.join(ROOT, "oracle", "_ref", "dropin")
+    # no warning comes from this build's headers
+    assert not re.search(r"model/(gpu_train|gpu_ops|hip_backend|trlm_host|trlm_ext)\.h", r.stderr), r.stderr[-3000:]
+    progs = ["training_train_lm_gpu", "training_generate", "training_chat", "training_train_lm",
+             "training_train_faz4", "training_train_faz5", "training_probe_batched_step", "tests_test_gpu_train",
+             "tests_test_gpu_ops", "tests_test_lm_model_gpu", "tests_test_batched_lm", "tests_test_data_parallel",
+             "tests_test_resume"]
+    for p in progs:
+        exe = os.path.join(out, p)
+        assert os.path.exists(exe), p
+        needed = subprocess.run(["readelf", "-d", exe], capture_output=True, text=True, check=True).stdout
+        assert "libtrlm_hip.so" in needed and "libcuda" not in needed, (p, needed)

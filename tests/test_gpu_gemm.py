@@ -219,8 +219,11 @@ MODEL = [  # name, M, N, K, ta, tb (row-major as the trainer lays them out)
     ("gate_up_fwd", 8192, 2048, 384, 0, 0),
     ("down_fwd", 8192, 384, 1024, 0, 0),
     ("qkv_dx", 8192, 384, 1152, 0, 1),
+    ("attn_out_dx", 8192, 384, 384, 0, 1),
+    ("gate_up_dx", 8192, 384, 2048, 0, 1),
     ("down_dx", 8192, 1024, 384, 0, 1),
     ("qkv_dw", 384, 1152, 8192, 1, 0),
+    ("attn_out_dw", 384, 384, 8192, 1, 0),
     ("gate_up_dw", 384, 2048, 8192, 1, 0),
     ("down_dw", 1024, 384, 8192, 1, 0),
 ]
@@ -233,6 +236,7 @@ def test_gemm_model_shapes(dev, name, M, N, K, ta, tb):
     B = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
     got, var = run_gemm(dev, A, B, ta, tb)
     ok, rel = close(got, ref64(A, B))
+    print("%s %s split %d: max err / max|C| = %.2e" % (name, var[0], var[1], rel))
     assert ok, (name, var, rel)
 
 
@@ -252,6 +256,42 @@ def test_gemm_lm_head_rows(dev):
     want = A[rows].astype(np.float64) @ E.T.astype(np.float64)
     ok, rel = close(got[rows], want)
     assert ok, rel
+
+
+def test_gemm_lm_head_backward_rows(dev):
+    """The LM head's two backward GEMMs at full size, in the trainer's layout
+    (logit rows padded to ld = 31772), checked against fp64 on samples:
+    dX = dlogits [8192, 31769] . E [31769, 384] (NN, K = 31769, split-K)
+    on 64 rows, and dW = dlogits^T . nf [31769, 8192] x [8192, 384] (TN,
+    M = 31769) on 64 rows, including the last one."""
+    rng = np.random.default_rng(21)
+    M, V, D, ld = 8192, 31769, 384, 31772
+    G = np.zeros((M, ld), np.float32)
+    G[:, :V] = rng.standard_normal((M, V), dtype=np.float32)
+    G[:, V:] = np.float32("nan")                  # padding columns are never read
+    E = (0.02 * rng.standard_normal((V, D))).astype(np.float32)
+    nf = rng.standard_normal((M, D)).astype(np.float32)
+    dG, dE, dnf = dev.upload(G), dev.upload(E), dev.upload(nf)
+    dX, dW = dev.empty(M * D * 4), dev.empty(V * D * 4)
+    try:
+        dev.matmul(0, 0, dG, dE, dX, M, D, V, ld, D, D)
+        var_x = dev.last_variant()
+        dev.matmul(1, 0, dG, dnf, dW, V, D, M, ld, D, D)
+        var_w = dev.last_variant()
+        gx = dev.download(dX, (M, D))
+        gw = dev.download(dW, (V, D))
+    finally:
+        for p in (dG, dE, dnf, dX, dW):
+            dev.free(p)
+    rows = np.sort(rng.choice(M, 64, replace=False))
+    ok, rel = close(gx[rows], G[rows, :V].astype(np.float64) @ E.astype(np.float64))
+    print("lm_head_dx %s split %d: %.2e" % (var_x[0], var_x[1], rel))
+    assert ok, (var_x, rel)
+    assert var_x[1] > 1, var_x
+    wrows = np.sort(np.concatenate([rng.choice(V - 1, 63, replace=False), [V - 1]]))
+    ok, rel = close(gw[wrows], G[:, wrows].T.astype(np.float64) @ nf.astype(np.float64))
+    print("lm_head_dw %s split %d: %.2e" % (var_w[0], var_w[1], rel))
+    assert ok, (var_w, rel)
 
 
 TILES = ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]

@@ -18,6 +18,8 @@ Checks per case:
 import numpy as np
 import pytest
 
+from conftest import parity_report
+
 pytestmark = pytest.mark.gpu
 
 CASES = {
@@ -77,11 +79,14 @@ def test_loss_and_grads(case):
     got = tr.grads()
     failures = []
     worst_all = 0.0
-    for i, (g, w) in enumerate(zip(model.split(got), model.split(case["grads"]))):
+    rows = [("loss", abs(float(loss) - float(case["loss"])), abs(float(case["loss"])))]
+    for i, (name, g, w) in enumerate(zip(model.names(), model.split(got), model.split(case["grads"]))):
         bad, worst = compare_tensor(g, w, TOL)
         worst_all = max(worst_all, worst)
+        rows.append((name, float(np.abs(g.astype(np.float64) - w).max()), float(np.abs(w).max())))
         if bad:
             failures.append((i, bad, w.size, worst))
+    parity_report("train_%s" % case["name"], rows)
     print("%s: loss gpu=%.7f cpu=%.7f worst rel grad err %.3e" % (case["name"], loss, case["loss"], worst_all))
     assert not failures, failures
 

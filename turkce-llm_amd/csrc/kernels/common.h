@@ -27,3 +27,16 @@ __device__ __forceinline__ double wave_sum_f64(double v) {
     for (int o = 32; o >= 1; o >>= 1) v += __shfl_xor(v, o, WAVE);
     return v;
 }
+
+// Greedy pick of one row, the rule of the reference's max scan
+// (generate.c:57-58: best starts at index 0 and moves only to a strictly
+// greater value).  Threads collect (value, index) with a strict > from
+// (-inf, ARGMAX_NONE), and reductions keep the larger value, the lower index
+// on ties, so NaNs are never picked; the result is then 0 when row[0] is NaN
+// (no value compares greater than it) or when nothing exceeded -inf.  Every
+// pick is a valid index, whatever the row holds.
+#define ARGMAX_NONE 0x7fffffff
+__device__ __forceinline__ int argmax_finish(const float* row, int idx) {
+    const float z0 = row[0];
+    return (z0 != z0 || idx == ARGMAX_NONE) ? 0 : idx;
+}

@@ -221,7 +221,7 @@ extern "C" __global__ void k_decode_advance(int* __restrict__ pos_dev) {
     if (threadIdx.x == 0 && blockIdx.x == 0) *pos_dev = *pos_dev + 1;
 }
 
-// Greedy pick per row (first index of the maximum, as k_argmax_rows), written
+// Greedy pick per row (argmax_finish's rule, as k_argmax_rows), written
 // both as the next step's input ids[row] and into hist[row*hist_ld + step]
 // with step = *pos_dev - pos_base, so generation needs no host round trip.
 #define ARGMAX_THREADS 1024
@@ -233,7 +233,7 @@ k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restr
     __shared__ int bi[NW];
     const float* z = logits + (long long)blockIdx.x * ld;
     float best = -INFINITY;
-    int idx = 0x7fffffff;
+    int idx = ARGMAX_NONE;
     // each thread scans its float4s in increasing index order, strict > keeps
     // the first occurrence; the reductions prefer the lower index on ties
     if ((ld & 3) == 0) {
@@ -264,6 +264,7 @@ k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restr
         int k = bi[0];
         for (int w = 1; w < NW; w++)
             if (bv[w] > b || (bv[w] == b && bi[w] < k)) { b = bv[w]; k = bi[w]; }
+        k = argmax_finish(z, k);
         ids[blockIdx.x] = (unsigned)k;
         hist[(long long)blockIdx.x * hist_ld + (*pos_dev - pos_base)] = (unsigned)k;
     }

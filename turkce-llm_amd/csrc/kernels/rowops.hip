@@ -381,14 +381,15 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     }
 }
 
-// First index of the row maximum (greedy decoding; ties -> lowest index).
+// Greedy pick per row: first index of the row maximum (ties -> lowest index),
+// NaN and all -inf rows as argmax_finish says.
 extern "C" __global__ void __launch_bounds__(256)
 k_argmax_rows(const float* __restrict__ logits, int ld, int V, unsigned* __restrict__ out) {
     __shared__ float bv[4];
     __shared__ int bi[4];
     const float* z = logits + (long long)blockIdx.x * ld;
     float best = -INFINITY;
-    int idx = 0x7fffffff;
+    int idx = ARGMAX_NONE;
     for (int j = threadIdx.x; j < V; j += 256) {
         float v = z[j];
         if (v > best) { best = v; idx = j; }
@@ -407,7 +408,7 @@ k_argmax_rows(const float* __restrict__ logits, int ld, int V, unsigned* __restr
         int k = bi[0];
         for (int w = 1; w < 4; w++)
             if (bv[w] > b || (bv[w] == b && bi[w] < k)) { b = bv[w]; k = bi[w]; }
-        out[blockIdx.x] = (unsigned)k;
+        out[blockIdx.x] = (unsigned)argmax_finish(z, k);
     }
 }
 
