@@ -52,6 +52,20 @@ void trlm_gemm_destroy(TrlmGemm* e);
 void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr);
+/* trlm_gemm for callers that cannot allocate device memory (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  It
+ * has no counterpart in the reference.  Same arguments, plan, kernels and
+ * results (bit for bit) as trlm_gemm on an engine from trlm_gemm_create,
+ * but the split-K partials go to a fixed 32 MiB scratch array that each GPU
+ * holds from the first trlm_gemm_create on it until the process ends, so
+ * the call allocates nothing.  Returns 0; or -1, with a message on stderr
+ * and nothing launched, when the shape's split-K plan needs more than
+ * 32 MiB (splits x (M+1) x N floats; of the model's GEMMs only the full-size
+ * LM-head dX does).  All calls on one GPU share its scratch: calls that
+ * overlap in time on one GPU (other streams, contexts or threads) race. */
+i32 trlm_gemm_noalloc(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+                      i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+                      f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr);
 /* Name of the kernel variant and split-K factor the last trlm_gemm call used. */
 const char* trlm_gemm_last_variant(TrlmGemm* e, i32* splits);
 /* The variant and split-K factor trlm_gemm picks for 16-byte-aligned operands

@@ -22,6 +22,7 @@ ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HSACO = os.path.join(HERE, "trlm_kernels.hsaco")
 LIB_HIP = os.path.join(HERE, "libtrlm_hip.so")
 LIB_HOST = os.path.join(HERE, "libtrlm_host.so")
+NOALLOC_O = os.path.join(HERE, "noalloc.o")
 
 # Packed-fp32 VALU ops are disabled for all device code.
 HIPCC_FLAGS = ["--genco", "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang",
@@ -47,9 +48,14 @@ def build_host():
 def build_hip_lib():
     srcs = [os.path.join(CSRC, f) for f in ("hip_backend.c", "trlm_gemm.c", "gpu_train.c", "gpu_decode.c", "checkpoint.c",
                                             "train_loop.c", "gpu_ops.c")]
+    # noalloc.hip holds the no-allocation GEMM's scratch array (a __device__
+    # global of this library, not of the kernel image) and its entry point.
+    _run([os.path.join(ROCM, "bin", "hipcc"), "-c", "-fPIC", "--offload-arch=gfx950", "-O3", "-Xclang",
+          "-target-feature", "-Xclang", "-packed-fp32-ops", "-I" + INC, os.path.join(CSRC, "noalloc.hip"),
+          "-o", NOALLOC_O])
     # Host-runtime symbols (allocator_alloc, tensor_*, pcg_*, m_*, rope_build_tables)
     # stay undefined: the reference's objects or libtrlm_host.so provide them.
-    _run(["gcc"] + CFLAGS + ["-shared"] + srcs +
+    _run(["gcc"] + CFLAGS + ["-shared"] + srcs + [NOALLOC_O] +
          ["-o", LIB_HIP, "-L" + os.path.join(ROCM, "lib"), "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-lamdhip64", "-pthread"])
 

@@ -9,6 +9,10 @@
 
 #pragma GCC visibility push(hidden)
 
+#ifdef __cplusplus
+extern "C" {
+#endif
+
 /* lm_collect_params order (model/gpu_train.c:8-13): [0] embedding; layer l
  * at 1 + 10*l + k; last = final norm weight. */
 enum { PK_ATTN_NORM = 0, PK_WQKV, PK_BQKV, PK_WO, PK_BO, PK_FFN_NORM, PK_WGU, PK_BGU, PK_WDOWN, PK_BDOWN };
@@ -55,6 +59,18 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                  f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x);
 
+/* trlm_gemm_ex with the split-K partials in a caller-given workspace of
+ * fixed_floats floats (fixed_ws != NULL): no allocation; returns -1, having
+ * launched nothing, when the plan needs more.  fixed_ws == NULL is
+ * trlm_gemm_ex (the engine's grow-only workspace). */
+i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+                 i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x,
+                 hipDeviceptr_t fixed_ws, u64 fixed_floats);
+/* noalloc.hip: resolves the device address of the GEMM scratch array on
+ * `device` (once per device; trlm_gemm_create calls it). */
+void trlm_noalloc_setup(i32 device);
+
 /* Queued driver steps (train_loop.c): see gpu_train.c. */
 void trlm_check_ids(const GpuTrainer* g, const u32* ids, const char* what);
 u32 trlm_embed_groups(GpuTrainer* g, const u32* ids, u32* order, u32* seg);
@@ -62,6 +78,10 @@ void trlm_train_step_queued(GpuTrainer* g, AdamOptimizer* opt, f32 weight_decay,
                             hipDeviceptr_t norm_out, hipDeviceptr_t scale_buf);
 void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc);
 void trlm_eval_queued(GpuTrainer* g, hipDeviceptr_t sum, i32 acc);
+
+#ifdef __cplusplus
+}
+#endif
 
 #pragma GCC visibility pop
 

@@ -87,6 +87,7 @@ TrlmGemm* trlm_gemm_create(HipCtx* ctx) {
         e->ku[l] = hip_get_kernel(ctx, name);
     }
     e->reduce = hip_get_kernel(ctx, "k_gemm_splitk_reduce");
+    trlm_noalloc_setup(ctx->device);
     return e;
 }
 
@@ -249,6 +250,14 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
 i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                  f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x) {
+    return trlm_gemm_ws(e, trans_a, trans_b, A, B, C, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta, bias,
+                        resid, ldr, x, NULL, 0);
+}
+
+i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
+                 i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
+                 f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x,
+                 hipDeviceptr_t fixed_ws, u64 fixed_floats) {
     hipDeviceptr_t stats = x ? x->stats : NULL, csum = x ? x->csum : NULL;
     i32 stats_cap = x ? x->stats_cap : 0;
     int rope = x && x->rope_cos;
@@ -323,13 +332,27 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
      * with column sums each split's slab has one more row, M, for them */
     u64 slab = ((u64)M + (csum ? 1u : 0u)) * (u64)N;
     u64 need = (u64)splits * slab;
-    if (need > e->ws_floats) {
-        if (e->ws) hip_free(e->ws);
-        e->ws = hip_alloc(need * sizeof(f32));
-        e->ws_floats = need;
+    hipDeviceptr_t W = fixed_ws;
+    if (fixed_ws) {
+        if (need > fixed_floats) {
+            fprintf(stderr,
+                    "[HIP ERROR] trlm_gemm_noalloc: %s with %d K splits needs %llu bytes of split-K workspace, "
+                    "more than the %llu-byte scratch; nothing was launched\n",
+                    e->last, splits, (unsigned long long)(need * sizeof(f32)),
+                    (unsigned long long)(fixed_floats * sizeof(f32)));
+            fflush(stderr);
+            return -1;
+        }
+    } else {
+        if (need > e->ws_floats) {
+            if (e->ws) hip_free(e->ws);
+            e->ws = hip_alloc(need * sizeof(f32));
+            e->ws_floats = need;
+        }
+        W = e->ws;
     }
     GemmParams q = p;
-    q.C = (float*)e->ws;
+    q.C = (float*)W;
     q.ldc = N;
     q.sW = (long long)slab;
     q.kchunk = kchunk;
@@ -337,7 +360,6 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
     q.alpha = 1.0f; q.beta = 0.0f; q.bias = NULL; q.resid = NULL;
     launch(e->k[layout][tile], &q, (u32)splits);
     long long total = (long long)slab;
-    hipDeviceptr_t W = e->ws;
     i32 sp = splits;
     i64 sW = (i64)slab;
     void* args[] = { &W, &sp, &sW, &C, &M, &N, &ldc, &alpha, &beta, &bias, &resid, &ldr, &csum };

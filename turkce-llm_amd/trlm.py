@@ -212,6 +212,10 @@ def _bind(host, hip):
                                   C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
                                   C.c_uint32, C.c_int64, C.c_int64, C.c_int64, C.c_float, C.c_float,
                                   C.c_void_p, C.c_void_p, C.c_int32])
+    _sig(hip, "trlm_gemm_noalloc", C.c_int32, [C.c_void_p, C.c_int32, C.c_int32, C.c_void_p, C.c_void_p,
+                                              C.c_void_p, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32,
+                                              C.c_int32, C.c_uint32, C.c_int64, C.c_int64, C.c_int64, C.c_float,
+                                              C.c_float, C.c_void_p, C.c_void_p, C.c_int32])
     _sig(hip, "trlm_gemm_last_variant", C.c_char_p, [C.c_void_p, C.POINTER(C.c_int32)])
     _sig(hip, "trlm_gemm_plan", C.c_char_p, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_uint32,
                                              C.POINTER(C.c_int32)])
@@ -529,6 +533,13 @@ class Device:
         self.hip.trlm_gemm(self.gemm, ta, tb, A, B, C_, M, N, K, lda, ldb, ldc, batch, sA, sB, sC, alpha, beta,
                            bias, resid, ldr or ldc)
 
+    def matmul_noalloc(self, ta, tb, A, B, C_, M, N, K, lda, ldb, ldc, batch=1, sA=0, sB=0, sC=0, alpha=1.0,
+                       beta=0.0, bias=None, resid=None, ldr=0):
+        """trlm_gemm_noalloc: returns 0, or -1 when the plan's split-K
+        workspace exceeds the 32 MiB scratch (nothing launched)."""
+        return self.hip.trlm_gemm_noalloc(self.gemm, ta, tb, A, B, C_, M, N, K, lda, ldb, ldc, batch, sA, sB, sC,
+                                          alpha, beta, bias, resid, ldr or ldc)
+
     def last_variant(self):
         sp = C.c_int32(0)
         name = self.hip.trlm_gemm_last_variant(self.gemm, C.byref(sp))
@@ -544,5 +555,6 @@ class Device:
         self.hip.hip_sync()
 
     def close(self):
+        self.current()   # the engine's workspace is freed in its own context
         self.hip.trlm_gemm_destroy(self.gemm)
         self.hip.hip_shutdown(C.byref(self.ctx))
