@@ -103,7 +103,7 @@ def test_undefined_symbols_are_runtime_only(trlm):
     other = {n for n in names if not (n.startswith("hip") or n.startswith("_") or n in runtime)}
     libc = {"fprintf", "fflush", "_exit", "fopen", "fseek", "ftell", "fread", "fclose", "malloc", "calloc",
             "realloc", "free", "memset", "memcpy", "memcmp", "strcmp", "strlen", "snprintf", "fwrite", "rename",
-            "remove", "stderr", "stdout", "clock_gettime",
+            "remove", "stderr", "stdout", "clock_gettime", "getenv",
             "pthread_mutex_lock", "pthread_mutex_unlock", "pthread_mutex_init", "pthread_mutex_destroy"}
     assert other <= libc, other - libc
     assert runtime & names == runtime, runtime - names
@@ -119,7 +119,7 @@ def test_code_object_has_every_kernel(trlm):
     names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_dvec_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
-    names |= {"k_decode_attn_hd%d" % d for d in (16, 32, 64)} | {"k_decode_merge_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_dec_attn_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in (
         "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32")}
     names |= {"k_gemm_%s_64x64_u" % l for l in ("nn", "nt", "tn", "tt")}

@@ -95,6 +95,35 @@ def test_mfma_lane_layout(trlm, dev):
     assert np.array_equal(out, want)
 
 
+def test_mfma16_lane_layout(trlm, dev):
+    """The lane layout the fused decode GEMMs (decode_fused.hip) assume for
+    v_mfma_f32_16x16x4f32: lane l holds A[l % 16][l / 16] and B[l / 16][l % 16];
+    result register r of lane l is D[4 (l / 16) + r][l % 16].  Exact with
+    small integers."""
+    hip = dev.hip
+    rng = np.random.default_rng(1)
+    a = rng.integers(-4, 5, 64).astype(np.float32)
+    b = rng.integers(-4, 5, 64).astype(np.float32)
+    da, db, dout = dev.upload(a), dev.upload(b), dev.empty(64 * 4 * 4)
+    f = hip.hip_get_kernel(C.byref(dev.ctx), b"k_mfma16_layout_probe")
+    pa, pb, po = C.c_void_p(da), C.c_void_p(db), C.c_void_p(dout)
+    args = (C.c_void_p * 3)(C.addressof(pa), C.addressof(pb), C.addressof(po))
+    hip.hip_launch(f, 1, 1, 1, 64, 1, 1, 0, args)
+    out = dev.download(dout, (64, 4))
+    A = np.zeros((16, 4)); B = np.zeros((4, 16))
+    for l in range(64):
+        A[l % 16, l // 16] = a[l]
+        B[l // 16, l % 16] = b[l]
+    D = A @ B
+    want = np.zeros((64, 4))
+    for l in range(64):
+        for r in range(4):
+            want[l, r] = D[4 * (l // 16) + r, l % 16]
+    for p in (da, db, dout):
+        dev.free(p)
+    assert np.array_equal(out, want)
+
+
 SMALL = [  # M, N, K
     (1, 1, 1), (4, 5, 3), (12, 150, 32), (65, 33, 17), (64, 64, 64), (127, 129, 130),
     (200, 96, 48), (31, 1000, 40), (128, 128, 16), (300, 200, 600), (96, 160, 1200),

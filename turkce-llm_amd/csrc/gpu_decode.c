@@ -9,10 +9,13 @@
  *            batch x len rows, with a per-layer hook that copies the rotated
  *            K and V into the cache; the LM head runs on the last row of
  *            each sequence only;
- *   step:    one new token per sequence -- the layer GEMMs on `batch` rows,
- *            RoPE at the token's position, append to the cache, attention of
- *            the new query over the cache (k_decode_attn_hd*, split over the
- *            context, merged in chunk order), head on `batch` rows.
+ *   step:    one new token per sequence, five fused kernels per layer
+ *            (kernels/decode_fused.hip): RMSNorm + QKV + RoPE + cache append;
+ *            attention over the cache in 128-key chunks, merged in chunk
+ *            order by the last chunk to finish; out-projection + residual;
+ *            RMSNorm + gate/up + SwiGLU; down-projection + residual; then the
+ *            final norm + LM head on `batch` rows.  Layer 0 reads its input
+ *            rows straight from the embedding table.
  * Greedy selection is the first maximum of each row (k_argmax_rows);
  * sampling is sample_next's arithmetic on the device (k_sample_rows) with the
  * uniform drawn from the caller's PCG stream on the host, as pcg_uniform does
@@ -30,31 +33,60 @@
 #include "gpu_internal.h"
 
 #define F4 ((u64)sizeof(f32))
-#define DEC_CHUNK 256u   /* keys per decode-attention block (<= 1024) */
+#define DEC_ATT_WAVES 8u   /* waves per decode-attention workgroup (as in decode_fused.hip) */
+#define DEC_HEAD_WAVES 8u  /* waves per LM-head workgroup (as in decode_fused.hip) */
+#define DEC_HEAD_KMAX 512u /* d_model bound of the LM-head kernel's LDS rows */
+
+/* Argument block of the fused decode GEMMs; layout identical to struct
+ * DecGemmParams in decode_fused.hip. */
+typedef struct DecGemmParams {
+    const float* A;
+    const u32* ids;
+    const float* E;
+    i32 a_ids, lda;
+    const float* W;
+    i32 ldw;
+    const float* bias;
+    const float* norm_w;
+    f32 eps;
+    const float* resid;
+    i32 resid_ids, ldr;
+    float* C;
+    i32 ldc;
+    i32 M, N, K;
+    i32 ncb;
+    i32 F;
+    const float* cos_t;
+    const float* sin_t;
+    const i32* pos;
+    i32 H, hd, D;
+    float* kc;
+    float* vc;
+    i32 ctx;
+    i32* pos_inc;
+} DecGemmParams;
 
 struct TrlmDecoder {
     GpuTrainer* g;
     u32 B, ctx, len;
     u32 L, H, hd, D, F, V, ldv;
-    u32 nsplit_max;
     f32 scale;
     hipDeviceptr_t kc, vc;              /* [L][B][H][ctx][hd] each */
     hipDeviceptr_t cos_t, sin_t;        /* [ctx][hd/2] */
     /* step buffers, B rows */
-    hipDeviceptr_t ids, x, x2, n, r, qkv, att, gu, h, nf, logits, part, out_ids;
+    hipDeviceptr_t ids, x, x2, qkv, att, h, nf, logits, out_ids;
     /* sampling scratch */
     hipDeviceptr_t e, prefix, u;
     /* prefill buffers, grown to batch x len rows on demand */
     u64 pre_rows;
     hipDeviceptr_t p_x, p_x2, p_n, p_r1, p_r2, p_qkv, p_att, p_lse, p_gu, p_h, p_nf, p_rf, p_ids;
-    hipFunction_t k_fill, k_append, k_attn, k_merge, k_gather, k_sample, k_advance, k_argmax_hist;
-    /* step replay: the position lives on the device (pos_dev), the attention
-     * grid is fixed at nsplit_max, and the step's GEMMs use the decoder's own
-     * engine, so every step is the same launch sequence -- captured once as
-     * a HIP graph after one eager step has sized the GEMM workspace */
+    hipFunction_t k_fill, k_gather, k_sample, k_argmax_hist;
+    hipFunction_t k_qkv, k_out, k_gu, k_down, k_head, k_attn;
+    /* step replay: the position lives on the device (pos_dev), so every step
+     * is the same launch sequence -- captured once as a HIP graph on the
+     * second step */
     hipDeviceptr_t pos_dev, hist;
     u32 hist_cap;
-    TrlmGemm* gemm;
     u32 eager_steps;
     hipGraph_t graph;
     hipGraphExec_t exec;
@@ -66,19 +98,30 @@ static void dec_fatal(const char* msg) {
     _exit(1);
 }
 
+static void check_hip(hipError_t e, const char* what) {
+    if (e != hipSuccess) {
+        fprintf(stderr, "[HIP ERROR] gpu_decode: %s -> %s: %s\n", what, hipGetErrorName(e), hipGetErrorString(e));
+        fflush(stderr);
+        _exit(1);
+    }
+}
+
 static u32 cdiv32(u64 a, u64 b) { return (u32)((a + b - 1) / b); }
 static hipDeviceptr_t fl(u64 floats) { return hip_alloc(floats * F4); }
 static hipDeviceptr_t at(hipDeviceptr_t base, u64 floats) { return (hipDeviceptr_t)((char*)base + floats * F4); }
 
 TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     if (batch == 0 || max_ctx == 0) dec_fatal("batch and max_ctx must be positive");
+    /* the fused step kernels take 16-column output blocks that never straddle
+     * a head or the q / k / v boundary, and 16-byte operand rows */
+    if (g->D % 16 || g->hd % 16 || g->F % 4 || g->D > DEC_HEAD_KMAX)
+        dec_fatal("decoding needs d_model and head_dim multiples of 16, d_model <= 512 and d_ff a multiple of 4");
     trlm_bind(g);
     TrlmDecoder* d = (TrlmDecoder*)calloc(1, sizeof(TrlmDecoder));
     d->g = g;
     d->B = batch; d->ctx = max_ctx; d->len = 0;
     d->L = g->L; d->H = g->H; d->hd = g->hd; d->D = g->D; d->F = g->F; d->V = g->V; d->ldv = g->ldv;
     d->scale = 1.0f / m_sqrtf((f32)g->hd);   /* attention.c:78 */
-    d->nsplit_max = cdiv32(max_ctx, DEC_CHUNK);
 
     u64 B = batch, D = g->D, F = g->F;
     u64 cache = (u64)g->L * B * g->H * max_ctx * g->hd;
@@ -87,16 +130,12 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->ids = hip_alloc(B * sizeof(u32));
     d->x = fl(B * D);
     d->x2 = fl(B * D);
-    d->n = fl(B * D);
-    d->r = fl(B);
-    d->qkv = fl(B * 3 * D);
+    d->qkv = fl(B * D);   /* the step's rotated queries */
     d->att = fl(B * D);
-    d->gu = fl(B * 2 * F);
     d->h = fl(B * F);
     d->nf = fl(B * D);
     d->logits = fl(B * g->ldv);
     hip_memset_zero(d->logits, B * g->ldv * F4);
-    d->part = fl(B * g->H * d->nsplit_max * (g->hd + 4));
     d->out_ids = hip_alloc(B * sizeof(u32));
     d->e = fl(B * g->V);
     d->prefix = hip_alloc(B * g->V * sizeof(f64));
@@ -128,17 +167,18 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     HipCtx* c = &g->hip;
     char name[64];
     d->k_fill = hip_get_kernel(c, "k_cache_fill");
-    d->k_append = hip_get_kernel(c, "k_decode_qkv_append");
-    snprintf(name, sizeof(name), "k_decode_attn_hd%u", g->hd);
-    d->k_attn = hip_get_kernel(c, name);
-    snprintf(name, sizeof(name), "k_decode_merge_hd%u", g->hd);
-    d->k_merge = hip_get_kernel(c, name);
     d->k_gather = hip_get_kernel(c, "k_gather_rows");
     d->k_sample = hip_get_kernel(c, "k_sample_rows");
-    d->k_advance = hip_get_kernel(c, "k_decode_advance");
     d->k_argmax_hist = hip_get_kernel(c, "k_argmax_hist");
+    d->k_qkv = hip_get_kernel(c, "k_dec_qkv");
+    d->k_out = hip_get_kernel(c, "k_dec_out");
+    d->k_gu = hip_get_kernel(c, "k_dec_gu");
+    d->k_down = hip_get_kernel(c, "k_dec_down");
+    d->k_head = hip_get_kernel(c, "k_dec_head");
+    snprintf(name, sizeof(name), "k_dec_attn_hd%u", g->hd);
+    d->k_attn = hip_get_kernel(c, name);
     d->pos_dev = hip_alloc(sizeof(i32));
-    d->gemm = trlm_gemm_create(c);
+    hip_sync();
     return d;
 }
 
@@ -163,9 +203,8 @@ void gpu_decoder_destroy(TrlmDecoder* d) {
     free_prefill(d);
     if (d->hist) hip_free(d->hist);
     hip_free(d->pos_dev);
-    trlm_gemm_destroy(d->gemm);
-    hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->n, d->r, d->qkv, d->att, d->gu, d->h, d->nf,
-                              d->logits, d->part, d->out_ids, d->e, d->prefix, d->u, d->cos_t, d->sin_t };
+    hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->qkv, d->att, d->h, d->nf,
+                              d->logits, d->out_ids, d->e, d->prefix, d->u, d->cos_t, d->sin_t };
     for (u32 i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) hip_free(bufs[i]);
     free(d);
 }
@@ -252,78 +291,123 @@ void gpu_decoder_prefill(TrlmDecoder* d, const u32* ids, u32 len) {
     hip_h2d(d->pos_dev, &lenv, sizeof(i32));
 }
 
-/* One decode step on the device: embed d->ids at position *pos_dev, the L
- * blocks with the cache append and decode attention, final norm, head into
- * d->logits, *pos_dev += 1.  Every argument is the same from step to step. */
+/* Workgroups of a fused decode GEMM: rt row tiles of 16*rb rows times the
+ * column blocks, rounded up to a multiple of the 8 XCDs (the kernel maps
+ * workgroup i to XCD i % 8 and skips the spare ones). */
+static void dec_gemm_launch(hipFunction_t f, DecGemmParams* p, u32 rb, u32 waves) {
+    u32 nrt = cdiv32((u64)p->M, 16u * rb), total = nrt * (u32)p->ncb;
+    u32 per_xcd = cdiv32(total, 8);
+    void* args[] = { p };
+    hip_launch(f, 8 * per_xcd, 1, 1, 64 * waves, 1, 1, 0, args);
+}
+
+/* One decode step on the device: the token d->ids of every sequence at
+ * position *pos_dev through the L layers and the head into d->logits, then
+ * *pos_dev += 1.  Every argument is the same from step to step. */
 static void step_body(TrlmDecoder* d) {
-    GpuTrainer ps = *d->g;   /* the trainer's kernels and parameters, the decoder's GEMM engine */
-    ps.gemm = d->gemm;
-    GpuTrainer* g = &ps;
-    const u32 B = d->B;
-    const i32 Bi = (i32)B, D = (i32)d->D, F = (i32)d->F, H = (i32)d->H, hd = (i32)d->hd, ldq = 3 * D;
-    const i32 ctxn = (i32)d->ctx, chunk = (i32)DEC_CHUNK, nsg = (i32)d->nsplit_max;
-    hipDeviceptr_t posd = d->pos_dev;
-    trlm_embed_rows(g, d->ids, d->x, B);
-    u64 per_layer = (u64)B * d->H * d->ctx * d->hd;
+    GpuTrainer* g = d->g;
+    const i32 Bc = (i32)d->B, D = (i32)d->D, F = (i32)d->F, H = (i32)d->H, hd = (i32)d->hd, ctxn = (i32)d->ctx;
+    const float* E = (const float*)trlm_param_ptr(g, 0);
+    const u64 per_layer = (u64)d->B * d->H * d->ctx * d->hd;
+    hipDeviceptr_t x = d->x, x2 = d->x2, q = d->qkv, att = d->att, h = d->h, logits = d->logits, posd = d->pos_dev;
+    DecGemmParams base;
+    memset(&base, 0, sizeof(base));
+    base.E = E;
+    base.ids = (const u32*)d->ids;
+    base.eps = g->eps;
+    base.M = Bc;
+    base.F = F;
+    base.H = H; base.hd = hd; base.D = D; base.ctx = ctxn;
+    base.cos_t = (const float*)d->cos_t; base.sin_t = (const float*)d->sin_t;
+    base.pos = (const i32*)posd;
     for (u32 l = 0; l < d->L; l++) {
-        hipDeviceptr_t kc = at(d->kc, l * per_layer), vc = at(d->vc, l * per_layer);
-#define PP(k) trlm_param_ptr(g, trlm_pidx(l, k))
-        trlm_rmsnorm_rows(g, d->x, PP(PK_ATTN_NORM), d->n, d->r, B);
-        trlm_gemm_rows(g, GEMM_NN, d->n, PP(PK_WQKV), d->qkv, Bi, 3 * D, D, D, 3 * D, 3 * D, PP(PK_BQKV), NULL);
+#define PP(k) ((const float*)trlm_param_ptr(g, trlm_pidx(l, k)))
+        float* kc = (float*)at(d->kc, l * per_layer);
+        float* vc = (float*)at(d->vc, l * per_layer);
+        /* q | k -> cache | v -> cache = RoPE(RMSNorm(x) @ Wqkv + b) */
+        DecGemmParams p = base;
+        p.A = (const float*)x; p.a_ids = l == 0; p.lda = D;
+        p.W = PP(PK_WQKV); p.ldw = 3 * D; p.bias = PP(PK_BQKV); p.norm_w = PP(PK_ATTN_NORM);
+        p.C = (float*)q; p.ldc = D;
+        p.N = 3 * D; p.K = D; p.ncb = (i32)cdiv32((u64)(3 * D), 16);
+        p.kc = kc; p.vc = vc;
+        dec_gemm_launch(d->k_qkv, &p, 1, 4);
         {
-            hipDeviceptr_t qkv = d->qkv, ct = d->cos_t, st = d->sin_t;
-            void* args[] = { &qkv, (void*)&ldq, &ct, &st, &posd, (void*)&Bi, (void*)&H, (void*)&hd, (void*)&D,
-                             &kc, &vc, (void*)&ctxn };
-            hip_launch(d->k_append, cdiv32((u64)B * d->H * (d->hd / 2), 256), 1, 1, 256, 1, 1, 0, args);
-        }
-        {
-            hipDeviceptr_t qkv = d->qkv, part = d->part, att = d->att;
+            hipDeviceptr_t kcp = kc, vcp = vc;
+            i32 ldq = D;
             f32 scale = d->scale;
-            void* args[] = { &qkv, (void*)&ldq, &kc, &vc, &posd, (void*)&ctxn, (void*)&H, (void*)&chunk, &scale,
-                             &part };
-            hip_launch(d->k_attn, B * d->H, d->nsplit_max, 1, 256, 1, 1, 0, args);
-            void* args2[] = { &part, &posd, (void*)&chunk, (void*)&nsg, (void*)&H, (void*)&D, &att };
-            hip_launch(d->k_merge, B * d->H, 1, 1, 64, 1, 1, 0, args2);
+            void* args[] = { &q, &ldq, &kcp, &vcp, &posd, (void*)&ctxn, (void*)&H, &scale, &att, (void*)&D };
+            hip_launch(d->k_attn, (u32)Bc * d->H, 1, 1, 64 * DEC_ATT_WAVES, 1, 1, 0, args);
         }
-        /* x2 = x + (att @ Wo + bo); x = x2 + (swiglu(norm(x2) @ Wgu + bgu) @ Wd + bd) */
-        trlm_gemm_rows(g, GEMM_NN, d->att, PP(PK_WO), d->x2, Bi, D, D, D, D, D, PP(PK_BO), d->x);
-        trlm_rmsnorm_rows(g, d->x2, PP(PK_FFN_NORM), d->n, d->r, B);
-        trlm_gemm_rows(g, GEMM_NN, d->n, PP(PK_WGU), d->gu, Bi, 2 * F, D, D, 2 * F, 2 * F, PP(PK_BGU), NULL);
-        trlm_swiglu_rows(g, d->gu, d->h, B);
-        trlm_gemm_rows(g, GEMM_NN, d->h, PP(PK_WDOWN), d->x, Bi, D, F, F, D, D, PP(PK_BDOWN), d->x2);
+        /* x2 = x + (att @ Wo + bo) */
+        p = base;
+        p.A = (const float*)att; p.lda = D;
+        p.W = PP(PK_WO); p.ldw = D; p.bias = PP(PK_BO);
+        p.resid = (const float*)x; p.resid_ids = l == 0; p.ldr = D;
+        p.C = (float*)x2; p.ldc = D;
+        p.N = D; p.K = D; p.ncb = (i32)cdiv32((u64)D, 16);
+        dec_gemm_launch(d->k_out, &p, 1, 4);
+        /* h = SwiGLU(RMSNorm(x2) @ Wgu + bgu) */
+        p = base;
+        p.A = (const float*)x2; p.lda = D;
+        p.W = PP(PK_WGU); p.ldw = 2 * F; p.bias = PP(PK_BGU); p.norm_w = PP(PK_FFN_NORM);
+        p.C = (float*)h; p.ldc = F;
+        p.N = 2 * F; p.K = D; p.ncb = (i32)cdiv32((u64)F, 16);
+        dec_gemm_launch(d->k_gu, &p, 1, 4);
+        /* x = x2 + (h @ Wd + bd) */
+        p = base;
+        p.A = (const float*)h; p.lda = F;
+        p.W = PP(PK_WDOWN); p.ldw = D; p.bias = PP(PK_BDOWN);
+        p.resid = (const float*)x2; p.ldr = D;
+        p.C = (float*)x; p.ldc = D;
+        p.N = D; p.K = F; p.ncb = (i32)cdiv32((u64)D, 16);
+        dec_gemm_launch(d->k_down, &p, 1, 8);
 #undef PP
     }
-    trlm_rmsnorm_rows(g, d->x, trlm_param_ptr(g, trlm_pidx(d->L, 0)), d->nf, d->r, B);
-    trlm_gemm_rows(g, GEMM_NT, d->nf, trlm_param_ptr(g, 0), d->logits, Bi, (i32)d->V, D, D, D, (i32)d->ldv, NULL,
-                   NULL);
-    void* args[] = { &posd };
-    hip_launch(d->k_advance, 1, 1, 1, 64, 1, 1, 0, args);
-}
-
-static void check_hip(hipError_t e, const char* what) {
-    if (e != hipSuccess) {
-        fprintf(stderr, "[HIP ERROR] gpu_decode: %s -> %s: %s\n", what, hipGetErrorName(e), hipGetErrorString(e));
-        fflush(stderr);
-        _exit(1);
+    /* logits = RMSNorm(x) @ E^T; the position moves on */
+    DecGemmParams p = base;
+    p.A = (const float*)x; p.a_ids = d->L == 0; p.lda = D;
+    p.W = E; p.ldw = D; p.norm_w = (const float*)trlm_param_ptr(g, trlm_pidx(d->L, 0));
+    p.C = (float*)logits; p.ldc = (i32)d->ldv;
+    p.N = (i32)d->V; p.K = D; p.ncb = (i32)cdiv32((u64)d->V, 16);
+    p.pos_inc = (i32*)posd;
+    {
+        /* persistent: at most one workgroup per CU (its rows fill most of the
+         * CU's LDS), each of its 8 waves walking column blocks */
+        u32 groups = cdiv32((u64)p.ncb, DEC_HEAD_WAVES);
+        if (groups > 256) groups = 256;
+        void* args[] = { &p };
+        hip_launch(d->k_head, groups, cdiv32((u64)Bc, 64), 1, 64 * DEC_HEAD_WAVES, 1, 1, 0, args);
     }
 }
 
-/* Runs one step: eagerly the first time (the GEMM engine sizes its
- * workspace), then as a replay of the step captured on the second call. */
+/* Steps run eagerly the first time, then as replays of the step captured on
+ * the second call.  With TRLM_DECODE_EAGER=1 in the environment every step runs eagerly --
+ * the same kernels in the same order, for kernel tracers (rocprofv3
+ * --kernel-trace faults on this ROCm while it intercepts a graph replay). */
+static int eager_only(void) {
+    static int v = -1;
+    if (v < 0) {
+        const char* e = getenv("TRLM_DECODE_EAGER");
+        v = (e && e[0] == '1') ? 1 : 0;
+    }
+    return v;
+}
+
 static void run_step(TrlmDecoder* d) {
-    if (d->exec) {
-        check_hip(hipGraphLaunch(d->exec, hip_current_stream()), "hipGraphLaunch");
-    } else if (d->eager_steps == 0) {
+    hipStream_t st = hip_current_stream();
+    if (eager_only() || d->eager_steps == 0) {
         step_body(d);
-        d->eager_steps++;
+    } else if (d->exec) {
+        check_hip(hipGraphLaunch(d->exec, st), "hipGraphLaunch");
     } else {
-        hipStream_t st = hip_current_stream();
         check_hip(hipStreamBeginCapture(st, hipStreamCaptureModeThreadLocal), "hipStreamBeginCapture");
         step_body(d);
         check_hip(hipStreamEndCapture(st, &d->graph), "hipStreamEndCapture");
         check_hip(hipGraphInstantiate(&d->exec, d->graph, NULL, NULL, 0), "hipGraphInstantiate");
         check_hip(hipGraphLaunch(d->exec, st), "hipGraphLaunch");
     }
+    d->eager_steps++;
 }
 
 void gpu_decoder_step(TrlmDecoder* d, const u32* ids) {

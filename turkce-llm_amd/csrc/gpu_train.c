@@ -96,11 +96,29 @@ static void rmsnorm_bwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDe
     hip_launch(g->k.rmsnorm_bwd, nb, 1, 1, 256, 1, 1, 4u * (u32)cols * (u32)F4, args);
 }
 
-/* dw = sum of an RMSNorm backward's partial rows, in block order. */
+#define COLSUM_GROUP 16u
+
+/* Rows of a partial buffer: the RMSNorm backward's per-block partials, then
+ * room for colsum_partials' group sums. */
+static u64 part_buffer_rows(u64 N) {
+    u64 nb = cdiv_u64(N, RMS_ROWS);
+    return nb + cdiv_u64(nb, COLSUM_GROUP);
+}
+
+/* dw = sum of an RMSNorm backward's partial rows: sums of 16-row groups in
+ * block order (one block per 64 columns x group, so the reduction spreads
+ * over the GPU), then the group sums in group order.  The group sums go to
+ * the partial buffer's own spare rows, so calls on different buffers may
+ * run concurrently. */
 static void colsum_partials(GpuTrainer* g, hipDeviceptr_t part, hipDeviceptr_t dw) {
-    i32 inb = (i32)cdiv_u64(g->N, RMS_ROWS), cols = (i32)g->D, acc = 0;
-    void* args[] = { &part, &inb, &cols, &dw, &acc };
-    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, args);
+    u32 nb = cdiv_u64(g->N, RMS_ROWS), ng = cdiv_u64(nb, COLSUM_GROUP);
+    i32 inb = (i32)nb, cols = (i32)g->D, acc = 0, grp = (i32)COLSUM_GROUP;
+    hipDeviceptr_t stage = (hipDeviceptr_t)((char*)part + (u64)nb * g->D * F4);
+    void* a1[] = { &part, &inb, &cols, &stage, &acc, &grp };
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), ng, 1, 256, 1, 1, 0, a1);
+    i32 ing = (i32)ng;
+    void* a2[] = { &stage, &ing, &cols, &dw, &acc, &ing };
+    hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, a2);
 }
 
 /* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
@@ -200,7 +218,7 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
         u64 nqb = ((u64)g.T + 63) / 64;
         g.att_ds = dalloc((u64)g.B * g.H * (nqb * (nqb + 1) / 2) * 4096);
     }
-    u64 part_rows = (N + RMS_ROWS - 1) / RMS_ROWS;   /* RMSNorm weight-gradient partials */
+    u64 part_rows = part_buffer_rows(N);   /* RMSNorm weight-gradient partials + their group sums */
     for (u32 i = 0; i < 4; i++) g.part[i / 2][i % 2] = dalloc(part_rows * D);
     g.part_final = dalloc(part_rows * D);
 

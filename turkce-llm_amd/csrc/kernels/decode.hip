@@ -7,20 +7,12 @@
 // token's projections plus one pass over the cached keys/values -- an HBM
 // bound pass (decode attention reads ctx*hd*8 bytes per head and sequence).
 //
-// Kernels:
+// Kernels (the step itself is in decode_fused.hip):
 //   k_cache_fill        prefill: copy K, V of a [B*len, 3D] qkv into the cache
-//   k_decode_qkv_append step: RoPE the new q, k at position pos (same
-//                       arithmetic as the QKV GEMM's RoPE epilogue), append k, v to the cache
-//   k_decode_attn_hd*   step: one (sequence, head, context chunk) per block;
-//                       writes the chunk's (max, sum, unnormalised O)
-//   k_decode_merge_hd*  step: combines the chunks in chunk order
-//   k_decode_advance    step: moves the device-resident position on
 //   k_argmax_hist       greedy generation: pick -> next ids and history
 //   k_gather_rows       last prompt row of every sequence
 //   k_sample_rows       sample_next (generate.c:57-73) on the device
 #include "common.h"
-
-#define DEC_LOG2E 1.4426950408889634f
 
 // kc/vc[((b*H + h)*ctx + t)*hd + d] = K/V of token t of sequence b, from
 // qkv[(b*len + t)*ldq + {D, 2D} + h*hd + d]; float4 per thread.
@@ -41,184 +33,6 @@ k_cache_fill(const float* __restrict__ qkv, int ldq, int B, int len, int H, int 
     long long dst = (((long long)b * H + h) * ctx + t) * hd + 4 * c;
     *(f32x4*)(kc + dst) = *(const f32x4*)(row + D);
     *(f32x4*)(vc + dst) = *(const f32x4*)(row + 2 * D);
-}
-
-// One thread per (sequence b, head h, pair k): rotate q and k of the new
-// token (row b of qkv) by position pos = *pos_dev as the QKV GEMM epilogue does,
-// write q back, append the rotated k and the v pair at cache position pos.
-// The position lives in device memory so that a captured step replays
-// unchanged (k_decode_advance moves it on).
-extern "C" __global__ void __launch_bounds__(256)
-k_decode_qkv_append(float* __restrict__ qkv, int ldq, const float* __restrict__ cos_t,
-                    const float* __restrict__ sin_t, const int* __restrict__ pos_dev, int B, int H, int hd, int D,
-                    float* __restrict__ kc, float* __restrict__ vc, int ctx) {
-    const int half = hd >> 1;
-    const int pos = *pos_dev;
-    int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= B * H * half) return;
-    int k = i % half, h = (i / half) % H, b = i / (half * H);
-    float c = cos_t[pos * half + k], s = sin_t[pos * half + k];
-    float* row = qkv + (long long)b * ldq;
-    float* q = row + h * hd + 2 * k;
-    float* kk = row + D + h * hd + 2 * k;
-    const float* v = row + 2 * D + h * hd + 2 * k;
-    float a0 = q[0], a1 = q[1];
-    q[0] = a0 * c - a1 * s;
-    q[1] = a0 * s + a1 * c;
-    a0 = kk[0]; a1 = kk[1];
-    long long dst = (((long long)b * H + h) * ctx + pos) * hd + 2 * k;
-    kc[dst] = a0 * c - a1 * s;
-    kc[dst + 1] = a0 * s + a1 * c;
-    vc[dst] = v[0];
-    vc[dst + 1] = v[1];
-}
-
-// grid (B*H, nsplit), 256 threads.  Block (bh, s) covers keys
-// [s*chunk, min((s+1)*chunk, n)) of sequence b, head h, for the query in
-// row b of qkv, with n = *pos_dev + 1 (blocks past n write an empty chunk).  Lanes work in groups of LPR = HD/4 lanes per key row
-// (float4 each, so a wave instruction reads whole rows, coalesced);
-// a wave takes every 4th group of RPI = 64/LPR rows.  Output per block:
-// part[(bh*nsplit + s)*(HD + 4) + {0..HD-1, HD, HD+1}] = O (unnormalised),
-// m (base-2 max of the scaled scores), l (sum of 2^(score - m)).
-// chunk <= 1024.  Every reduction has a fixed order.
-template <int HD>
-__device__ void decode_attn(const float* __restrict__ qkv, int ldq, const float* __restrict__ kc,
-                            const float* __restrict__ vc, const int* __restrict__ pos_dev, int ctx, int H, int chunk,
-                            float scale, float* __restrict__ part) {
-    const int n = *pos_dev + 1;
-    constexpr int LPR = HD / 4, RPI = 64 / LPR;
-    __shared__ float sc[1024];
-    __shared__ float red[8];
-    __shared__ f32x4 oacc[4][LPR];
-    const int bh = blockIdx.x, s = blockIdx.y, nsplit = gridDim.y;
-    const int b = bh / H, h = bh - b * H;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / LPR, c4 = lane % LPR;
-    const int k0 = s * chunk;
-    int k1 = k0 + chunk;
-    if (k1 > n) k1 = n;
-    const int cnt = k1 > k0 ? k1 - k0 : 0;
-    const float c2 = scale * DEC_LOG2E;
-    const long long cbase = ((long long)bh * ctx) * HD;
-    const f32x4 q = *(const f32x4*)(qkv + (long long)b * ldq + h * HD + 4 * c4);
-
-    // scores: a wave's rows of NIT iterations are loaded together (their
-    // latency overlaps), then reduced across the LPR lanes of each row
-    constexpr int NIT = 256 / (4 * RPI);
-    for (int g0 = 0; g0 < cnt; g0 += NIT * 4 * RPI) {
-        f32x4 kv[NIT];
-#pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
-            kv[it] = j < cnt ? *(const f32x4*)(kc + cbase + (long long)(k0 + j) * HD + 4 * c4)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
-            float d = kv[it][0] * q[0] + kv[it][1] * q[1] + kv[it][2] * q[2] + kv[it][3] * q[3];
-#pragma unroll
-            for (int o = 1; o < LPR; o <<= 1) d += __shfl_xor(d, o, WAVE);
-            if (c4 == 0 && j < cnt) sc[j] = d * c2;
-        }
-    }
-    __syncthreads();
-    // max and sum of 2^(score - max) over the chunk (fixed order)
-    float mx = -INFINITY;
-    for (int j = threadIdx.x; j < cnt; j += 256) mx = fmaxf(mx, sc[j]);
-    mx = wave_max(mx);
-    if (lane == 0) red[wave] = mx;
-    __syncthreads();
-    mx = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-    float ls = 0.f;
-    for (int j = threadIdx.x; j < cnt; j += 256) {
-        float e = exp2f(sc[j] - mx);
-        sc[j] = e;
-        ls += e;
-    }
-    ls = wave_sum(ls);
-    if (lane == 0) red[4 + wave] = ls;
-    __syncthreads();
-    // O = sum_j p_j V_j
-    f32x4 o = {0.f, 0.f, 0.f, 0.f};
-    for (int g0 = 0; g0 < cnt; g0 += NIT * 4 * RPI) {
-        f32x4 vv[NIT];
-#pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
-            vv[it] = j < cnt ? *(const f32x4*)(vc + cbase + (long long)(k0 + j) * HD + 4 * c4)
-                             : f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-#pragma unroll
-        for (int it = 0; it < NIT; it++) {
-            const int j = g0 + it * 4 * RPI + wave * RPI + sub;
-            if (j < cnt) o += sc[j] * vv[it];
-        }
-    }
-#pragma unroll
-    for (int w = LPR; w < 64; w <<= 1) {
-        o[0] += __shfl_xor(o[0], w, WAVE);
-        o[1] += __shfl_xor(o[1], w, WAVE);
-        o[2] += __shfl_xor(o[2], w, WAVE);
-        o[3] += __shfl_xor(o[3], w, WAVE);
-    }
-    if (sub == 0) oacc[wave][c4] = o;
-    __syncthreads();
-    float* dst = part + ((long long)bh * nsplit + s) * (HD + 4);
-    if (threadIdx.x < LPR) {
-        f32x4 t = oacc[0][threadIdx.x];
-        t += oacc[1][threadIdx.x];
-        t += oacc[2][threadIdx.x];
-        t += oacc[3][threadIdx.x];
-        *(f32x4*)(dst + 4 * threadIdx.x) = t;
-    }
-    if (threadIdx.x == 0) {
-        dst[HD] = mx;
-        dst[HD + 1] = ((red[4] + red[5]) + red[6]) + red[7];
-    }
-}
-
-// One wave per (sequence, head): att[b, h*HD + d] = sum_s w_s O_s[d] /
-// sum_s w_s l_s with w_s = 2^(m_s - max_s m_s), over the chunks that hold
-// keys (n = *pos_dev + 1), in order; records are nsplit_grid per head.
-template <int HD>
-__device__ void decode_merge(const float* __restrict__ part, const int* __restrict__ pos_dev, int chunk,
-                             int nsplit_grid, int H, int D, float* __restrict__ att) {
-    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-    const int d = threadIdx.x;
-    const int nsplit = (*pos_dev + chunk) / chunk;
-    const float* p = part + (long long)bh * nsplit_grid * (HD + 4);
-    float M = -INFINITY;
-    for (int s = 0; s < nsplit; s++) M = fmaxf(M, p[s * (HD + 4) + HD]);
-    float L = 0.f, o = 0.f;
-    for (int s = 0; s < nsplit; s++) {
-        const float m = p[s * (HD + 4) + HD];
-        const float w = (m == -INFINITY) ? 0.f : exp2f(m - M);
-        L += w * p[s * (HD + 4) + HD + 1];
-        if (d < HD) o += w * p[s * (HD + 4) + d];
-    }
-    if (d < HD) att[(long long)b * D + h * HD + d] = o / L;
-}
-
-#define DECODE_KERNELS(HD)                                                                                  \
-    extern "C" __global__ void __launch_bounds__(256)                                                       \
-    k_decode_attn_hd##HD(const float* qkv, int ldq, const float* kc, const float* vc, const int* pos_dev,   \
-                         int ctx, int H, int chunk, float scale, float* part) {                             \
-        decode_attn<HD>(qkv, ldq, kc, vc, pos_dev, ctx, H, chunk, scale, part);                             \
-    }                                                                                                       \
-    extern "C" __global__ void __launch_bounds__(64)                                                        \
-    k_decode_merge_hd##HD(const float* part, const int* pos_dev, int chunk, int nsplit_grid, int H, int D,  \
-                          float* att) {                                                                     \
-        decode_merge<HD>(part, pos_dev, chunk, nsplit_grid, H, D, att);                                     \
-    }
-
-DECODE_KERNELS(16)
-DECODE_KERNELS(32)
-DECODE_KERNELS(64)
-
-// *pos_dev += 1: the step's token is in the cache.
-extern "C" __global__ void k_decode_advance(int* __restrict__ pos_dev) {
-    if (threadIdx.x == 0 && blockIdx.x == 0) *pos_dev = *pos_dev + 1;
 }
 
 // Greedy pick per row (argmax_finish's rule, as k_argmax_rows), written

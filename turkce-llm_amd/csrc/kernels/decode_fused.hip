@@ -1,0 +1,505 @@
+// decode_fused.hip -- the KV-cache decode step as five kernels per layer.
+//
+// A decode step runs the model on one new token per sequence: every product
+// has only `batch` rows (64 in the benchmark), so the step is bound by
+// latency and HBM, not by the matrix cores.  The reference computes it as
+// the full-window lm_forward (training/generate.c:186-212); within the
+// context the last row needs only the cached keys and values, so a step is:
+//   k_dec_qkv   RMSNorm(x) @ Wqkv + b, RoPE on q and k at the position,
+//               k and v appended to the cache, q kept       (layer 0: x = E[ids])
+//   k_dec_attn  q over the cached keys: a workgroup per (sequence, head),
+//               its 8 waves splitting the context, merged in wave order
+//   k_dec_out   x2 = x + (att @ Wo + bo)
+//   k_dec_gu    h = SwiGLU(RMSNorm(x2) @ Wgu + bgu)
+//   k_dec_down  x = x2 + (h @ Wd + bd)
+//   k_dec_head  logits = RMSNorm(x) @ E^T, then the position moves on
+//
+// GEMM tiling.  The output is cut into 16 x 16 blocks, one per workgroup
+// (two for the gate/up pair), so even a 64-row product spreads over
+// hundreds of CUs; the workgroup's KW waves split K, each accumulating its
+// share with v_mfma_f32_16x16x4f32, and the partial blocks are added in wave
+// order through LDS.  Workgroups are mapped so that each XCD takes a
+// contiguous range of column blocks (the weight slices it streams share its
+// L2 with its neighbours').  Operands are read straight from global memory,
+// 16 bytes per lane: lane (i, kq) of a wave holds A[row i][k0 + 4kq .. +3]
+// and feeds component u to MFMA step u, i.e. the MFMA's k index kq at step u
+// stands for k0 + 4kq + u; the B operand is read with the same mapping, so
+// the dot products are unchanged.
+//
+// RMSNorm is applied as out[m, n] = r[m] * sum_k (x[m, k] w[k]) W[k, n] with
+// r = 1/sqrt(mean(x^2) + eps) taken in f64 (as the reference's
+// k_rmsnorm_fwd), the waves' sums of squares added in wave order.
+#include "common.h"
+
+typedef float f32x4_t __attribute__((ext_vector_type(4)));
+
+#define DEC_LOG2E_F 1.4426950408889634f
+
+enum { DM_PLAIN = 0, DM_QKV = 1, DM_SWIGLU = 2 };
+
+// Argument block of the fused GEMMs; layout mirrored by DecGemmParams in
+// gpu_decode.c.
+struct DecGemmParams {
+    const float* A;          // [M, lda] (unused when a_ids)
+    const unsigned* ids;     // token ids [M] for a_ids / resid_ids
+    const float* E;          // embedding table [V, D] for ids
+    int a_ids;               // row m of A is E[ids[m]] (layer 0's input), row stride lda
+    int lda;
+    const float* W;          // NN: [K, ldw]; NT: [N, ldw] (the head's E)
+    int ldw;
+    const float* bias;       // [N] or null
+    const float* norm_w;     // RMSNorm weight [K] (kernels with the norm prologue)
+    float eps;
+    const float* resid;      // [M, ldr] or null
+    int resid_ids;           // row m of resid is E[ids[m]] (layer 0), row stride ldr
+    int ldr;
+    float* C;                // [M, ldc]
+    int ldc;
+    int M, N, K;
+    int ncb;                 // column blocks of 16
+    int F;                   // SwiGLU: the up half starts at column F; h has F columns
+    const float* cos_t;      // QKV: RoPE tables [ctx][hd/2]
+    const float* sin_t;
+    const int* pos;          // the token's position (device-resident)
+    int H, hd, D;
+    float* kc;               // this layer's caches [M][H][ctx][hd]
+    float* vc;
+    int ctx;
+    int* pos_inc;            // head: block 0 adds 1 to *pos_inc after its stores
+};
+
+__device__ __forceinline__ f32x4_t ld4(const float* p) { return *(const f32x4_t*)p; }
+
+template <int KW, int RB, bool NT, int MODE, bool NORM>
+__device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
+    constexpr int NACC = (MODE == DM_SWIGLU) ? 2 : 1;   // gate and up blocks
+    __shared__ float red[KW][RB * NACC][4][64];
+    __shared__ float ssq[KW][RB * 16];
+    __shared__ float rn[RB * 16];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int li = lane & 15, kq = lane >> 4;
+
+    // workgroup -> (row tile, column block): XCD x = blockIdx.x % 8 takes a
+    // contiguous range of column blocks, its row tiles next to each other
+    const int nrt = (p.M + 16 * RB - 1) / (16 * RB);
+    const int total = nrt * p.ncb;
+    const int per_xcd = (total + 7) >> 3;
+    const int t = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+    if (t >= total) return;
+    const int rt = t % nrt, cb = t / nrt;
+    const int m0 = rt * 16 * RB;
+
+    // this wave's k range: a multiple of 16 per wave
+    const int kper = (((p.K + KW - 1) / KW) + 15) & ~15;
+    const int k0 = w * kper;
+    int k1 = k0 + kper;
+    if (k1 > p.K) k1 = p.K;
+
+    // A rows this lane reads (clamped to valid rows; their results are not stored)
+    const float* arow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        int m = m0 + 16 * rb + li;
+        if (m > p.M - 1) m = p.M - 1;
+        arow[rb] = p.a_ids ? p.E + (long long)p.ids[m] * p.lda : p.A + (long long)m * p.lda;
+    }
+    // B columns this lane reads (clamped; masked below)
+    const int ncols = (MODE == DM_SWIGLU) ? p.F : p.N;
+    const int c = 16 * cb + li;
+    const bool cvalid = c < ncols;
+    int bcol[NACC];
+    bcol[0] = cvalid ? c : 0;
+    if (NACC == 2) bcol[NACC - 1] = cvalid ? p.F + c : 0;
+
+    // wave 0's epilogue inputs, loaded now so they arrive with the operands:
+    // bias, residual rows (this lane's 4 rows per row block), and for the
+    // QKV epilogue the position and this lane's RoPE pair
+    float ebias[NACC], eres[RB][4], ecs = 1.f, esn = 0.f;
+    int pos = 0;
+    if (w == 0) {
+#pragma unroll
+        for (int a = 0; a < NACC; a++) ebias[a] = p.bias ? p.bias[bcol[a]] : 0.f;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                eres[rb][r] = 0.f;
+                if (MODE == DM_PLAIN && (p.resid || p.resid_ids)) {
+                    int m = m0 + 16 * rb + 4 * kq + r;
+                    if (m > p.M - 1) m = p.M - 1;
+                    eres[rb][r] = p.resid_ids ? p.E[(long long)p.ids[m] * p.ldr + bcol[0]]
+                                              : p.resid[(long long)m * p.ldr + bcol[0]];
+                }
+            }
+        if (MODE == DM_QKV) {
+            pos = *p.pos;
+            const int dcol = c - (c / p.D) * p.D, d = dcol % p.hd, half = p.hd >> 1;
+            ecs = p.cos_t[pos * half + (d >> 1)];
+            esn = p.sin_t[pos * half + (d >> 1)];
+        }
+    }
+
+    f32x4_t acc[RB][NACC];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int a = 0; a < NACC; a++) acc[rb][a] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    float ss[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) ss[rb] = 0.f;
+
+    // batches of up to 8 k-blocks of 16: every load of a batch is issued
+    // (unconditionally, from clamped valid addresses) before any of its
+    // arithmetic -- a load under a branch would be waited for inside it --
+    // then lanes past K or N are zeroed, the norm weight applied, and the
+    // MFMAs issued
+    for (int kb = k0; kb < k1; kb += 128) {
+        f32x4_t av[8][RB];
+        f32x4_t bv[8][NACC];
+        f32x4_t nw[8];
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const int k = kb + 16 * j + 4 * kq;
+            const int ks = k < k1 ? k : 0;
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) av[j][rb] = ld4(arow[rb] + ks);
+#pragma unroll
+            for (int a = 0; a < NACC; a++) {
+                if (NT) {
+                    bv[j][a] = ld4(p.W + (long long)bcol[a] * p.ldw + ks);
+                } else {
+                    const float* wp = p.W + (long long)ks * p.ldw + bcol[a];
+#pragma unroll
+                    for (int u = 0; u < 4; u++) bv[j][a][u] = wp[(long long)u * p.ldw];
+                }
+            }
+            if (NORM) nw[j] = ld4(p.norm_w + ks);
+        }
+        const f32x4_t zero = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            const bool kv = kb + 16 * j + 4 * kq < k1;
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                const f32x4_t x = kv ? av[j][rb] : zero;
+                if (NORM) {
+                    ss[rb] += x[0] * x[0] + x[1] * x[1] + x[2] * x[2] + x[3] * x[3];
+                    av[j][rb] = x * nw[j];
+                } else {
+                    av[j][rb] = x;
+                }
+            }
+#pragma unroll
+            for (int a = 0; a < NACC; a++) bv[j][a] = (kv && cvalid) ? bv[j][a] : zero;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int u = 0; u < 4; u++)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                    for (int a = 0; a < NACC; a++)
+                        acc[rb][a] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[j][rb][u], bv[j][a][u], acc[rb][a], 0, 0, 0);
+    }
+
+    // partial blocks -> LDS; wave 0 adds them in wave order
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int a = 0; a < NACC; a++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) red[w][rb * NACC + a][r][lane] = acc[rb][a][r];
+    if (NORM) {
+        // sum of squares of row li over this wave's k range: the four kq lane groups
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            float s = ss[rb];
+            s += __shfl_xor(s, 16, WAVE);
+            s += __shfl_xor(s, 32, WAVE);
+            if (kq == 0) ssq[w][rb * 16 + li] = s;
+        }
+    }
+    __syncthreads();
+    if (NORM && threadIdx.x < RB * 16) {
+        float s = ssq[0][threadIdx.x];
+#pragma unroll
+        for (int q = 1; q < KW; q++) s += ssq[q][threadIdx.x];
+        rn[threadIdx.x] = 1.0f / (float)sqrt((double)(s / (float)p.K + p.eps));
+    }
+    __syncthreads();
+    if (w != 0) return;
+
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        float v[NACC][4];
+#pragma unroll
+        for (int a = 0; a < NACC; a++)
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                float s = red[0][rb * NACC + a][r][lane];
+#pragma unroll
+                for (int q = 1; q < KW; q++) s += red[q][rb * NACC + a][r][lane];
+                v[a][r] = s;
+            }
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const int mrow = 16 * rb + 4 * kq + r;   // row within the tile (result layout of the MFMA)
+            const int m = m0 + mrow;
+            const float scale = NORM ? rn[mrow] : 1.0f;
+            float o[NACC];
+#pragma unroll
+            for (int a = 0; a < NACC; a++) o[a] = v[a][r] * scale + ebias[a];
+            if (MODE == DM_QKV) {
+                // columns of q | k | v; RoPE pairs (2k, 2k+1) are neighbouring lanes
+                const float partner = __shfl_xor(o[0], 1, WAVE);
+                const int reg = c / p.D, dcol = c - reg * p.D;
+                const int h = dcol / p.hd, d = dcol - h * p.hd;
+                float val = o[0];
+                if (reg < 2) val = (d & 1) ? partner * esn + o[0] * ecs : o[0] * ecs - partner * esn;
+                if (m < p.M && cvalid) {
+                    if (reg == 0) {
+                        p.C[(long long)m * p.ldc + dcol] = val;
+                    } else {
+                        float* cache = reg == 1 ? p.kc : p.vc;
+                        cache[(((long long)m * p.H + h) * p.ctx + pos) * p.hd + d] = val;
+                    }
+                }
+            } else if (MODE == DM_SWIGLU) {
+                const float g = o[0], u = o[NACC - 1];
+                const float sg = 1.0f / (1.0f + expf(-g));
+                if (m < p.M && cvalid) p.C[(long long)m * p.ldc + c] = (g * sg) * u;
+            } else {
+                if (m < p.M && cvalid) p.C[(long long)m * p.ldc + c] = (p.resid || p.resid_ids) ? eres[rb][r] + o[0] : o[0];
+            }
+        }
+    }
+    if (p.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *p.pos_inc = *p.pos_inc + 1;
+}
+
+extern "C" __global__ void __launch_bounds__(256) k_dec_qkv(DecGemmParams p) { dec_gemm<4, 1, false, DM_QKV, true>(p); }
+extern "C" __global__ void __launch_bounds__(256) k_dec_out(DecGemmParams p) { dec_gemm<4, 1, false, DM_PLAIN, false>(p); }
+extern "C" __global__ void __launch_bounds__(256) k_dec_gu(DecGemmParams p) { dec_gemm<4, 1, false, DM_SWIGLU, true>(p); }
+extern "C" __global__ void __launch_bounds__(512) k_dec_down(DecGemmParams p) { dec_gemm<8, 1, false, DM_PLAIN, false>(p); }
+
+// ---------------------------------------------------------------- LM head
+// logits[m, n] = sum_k (x[m, k] r[m] w[k]) E[n, k] for the (up to) 64 rows of
+// row tile blockIdx.y, with r the row's RMSNorm reciprocal.  A persistent
+// grid: each workgroup first writes its rows' normalised values
+// (x * r * w, elementwise as the reference's norm) into LDS, once; then each
+// of its 8 waves walks column blocks of 16 vocabulary rows over the whole of
+// K, four 16-row MFMA blocks sharing every E fragment, with the next 64-deep
+// chunk of E loaded while the current one's 64 MFMAs issue.  LDS rows are
+// padded by 4 floats so the 16 rows of a fragment read fall in different
+// banks.  K <= DEC_HEAD_KMAX, K % 16 == 0.
+#define DEC_HEAD_KMAX 512
+#define DEC_HEAD_WAVES 8
+extern "C" __global__ void __launch_bounds__(64 * DEC_HEAD_WAVES) k_dec_head(DecGemmParams p) {
+    constexpr int LDK = DEC_HEAD_KMAX + 4;
+    __shared__ float xs[64 * LDK];
+    __shared__ float rs[64];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    const int li = lane & 15, kq = lane >> 4;
+    const int m0 = blockIdx.y * 64;
+    const int K = p.K, K4 = K >> 2;
+    // rows m0 .. m0+63 (clamped) -> sums of squares: wave w takes rows w, w+8, ...
+    for (int rr = w; rr < 64; rr += DEC_HEAD_WAVES) {
+        int m = m0 + rr;
+        if (m > p.M - 1) m = p.M - 1;
+        const float* xr = p.a_ids ? p.E + (long long)p.ids[m] * p.lda : p.A + (long long)m * p.lda;
+        float ss = 0.f;
+        for (int q = lane; q < K4; q += 64) {
+            const f32x4_t v = ld4(xr + 4 * q);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+            *(f32x4_t*)(xs + rr * LDK + 4 * q) = v;
+        }
+        ss = wave_sum(ss);
+        if (lane == 0) rs[rr] = 1.0f / (float)sqrt((double)(ss / (float)K + p.eps));
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < 64 * K4; i += 64 * DEC_HEAD_WAVES) {
+        const int rr = i / K4, q = i - rr * K4;
+        const f32x4_t wv = ld4(p.norm_w + 4 * q);
+        f32x4_t v = *(f32x4_t*)(xs + rr * LDK + 4 * q);
+        const float r = rs[rr];
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[e] = v[e] * r * wv[e];
+        *(f32x4_t*)(xs + rr * LDK + 4 * q) = v;
+    }
+    __syncthreads();
+
+    const int nwaves = gridDim.x * DEC_HEAD_WAVES;
+    for (int cb = blockIdx.x * DEC_HEAD_WAVES + w; cb < p.ncb; cb += nwaves) {
+        const int c = 16 * cb + li;
+        const bool cvalid = c < p.N;
+        const float* er = p.W + (long long)(cvalid ? c : 0) * p.ldw + 4 * kq;
+        f32x4_t acc[4];
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) acc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        // 16-deep steps past K (K % 16 == 0) load a valid k step and are skipped
+        f32x4_t bn[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) bn[j] = ld4(er + (16 * j < K ? 16 * j : 0));
+        for (int k0 = 0; k0 < K; k0 += 64) {
+            f32x4_t bv[4];
+#pragma unroll
+            for (int j = 0; j < 4; j++) bv[j] = bn[j];
+            if (k0 + 64 < K) {
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const int kn = k0 + 64 + 16 * j;
+                    bn[j] = ld4(er + (kn < K ? kn : 0));
+                }
+            }
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                if (k0 + 16 * j >= K) break;
+                f32x4_t av[4];
+#pragma unroll
+                for (int rb = 0; rb < 4; rb++) av[rb] = *(const f32x4_t*)(xs + (16 * rb + li) * LDK + k0 + 16 * j + 4 * kq);
+#pragma unroll
+                for (int u = 0; u < 4; u++)
+#pragma unroll
+                    for (int rb = 0; rb < 4; rb++)
+                        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb][u], bv[j][u], acc[rb], 0, 0, 0);
+            }
+        }
+        if (cvalid) {
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + 16 * rb + 4 * kq + r;
+                    if (m < p.M) p.C[(long long)m * p.ldc + c] = acc[rb][r];
+                }
+        }
+    }
+    if (p.pos_inc && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *p.pos_inc = *p.pos_inc + 1;
+}
+
+// ---------------------------------------------------------------- attention
+// One workgroup of 8 waves per (sequence b, head h), for the query
+// q[b, h*HD ..] over the n = *pos + 1 cached keys.  Wave w takes the keys
+// [w*per, (w+1)*per) and walks them in passes of 8*RPI rows, with an online
+// softmax (base-2 running max, rescaled sum and O); lanes work in groups of
+// LPR = HD/4 lanes per key row (float4 each, whole rows per wave
+// instruction), and a pass's K and V rows are all loaded before any
+// arithmetic.  The 8 waves' (max, sum, O) are merged through LDS in wave
+// order, so the result is deterministic; no workgroup waits for another.
+#define DEC_ATT_WAVES 8
+template <int HD, int WAVES = DEC_ATT_WAVES, int NIT = 4>
+__device__ __forceinline__ void dec_attn(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
+                                         const float* __restrict__ vc, const int* __restrict__ pos_dev, int ctx,
+                                         int H, float scale, float* __restrict__ att, int D) {
+    constexpr int LPR = HD / 4, RPI = 64 / LPR, PASS = NIT * RPI;
+    __shared__ float wm[WAVES], wl[WAVES];
+    __shared__ f32x4_t wo[WAVES][LPR];
+    const int n = *pos_dev + 1;
+    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LPR, c4 = lane % LPR;
+    const int per = ((n + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;
+    const int j0 = wave * per;
+    int j1 = j0 + per;
+    if (j1 > n) j1 = n;
+    const float c2 = scale * DEC_LOG2E_F;
+    const float* kb = kc + (long long)bh * ctx * HD + 4 * c4;
+    const float* vb = vc + (long long)bh * ctx * HD + 4 * c4;
+    const f32x4_t qv = ld4(q + (long long)b * ldq + h * HD + 4 * c4);
+
+    float mx = -INFINITY, ls = 0.f;
+    f32x4_t o = {0.f, 0.f, 0.f, 0.f};
+    // pass p's rows are loaded during pass p-1's arithmetic; loads are
+    // unconditional, from clamped rows (row 0 always holds a key)
+    f32x4_t kn[NIT], vn[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int j = j0 + it * RPI + sub;
+        const long long off = (long long)(j < j1 ? j : 0) * HD;
+        kn[it] = ld4(kb + off);
+        vn[it] = ld4(vb + off);
+    }
+    for (int p0 = j0; p0 < j1; p0 += PASS) {
+        f32x4_t kr[NIT], vr[NIT];
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            kr[it] = kn[it];
+            vr[it] = vn[it];
+            const int j = p0 + PASS + it * RPI + sub;
+            const long long off = (long long)(j < j1 ? j : 0) * HD;
+            kn[it] = ld4(kb + off);
+            vn[it] = ld4(vb + off);
+        }
+        float sc[NIT];
+        float pm = -INFINITY;
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const int j = p0 + it * RPI + sub;
+            float d = kr[it][0] * qv[0] + kr[it][1] * qv[1] + kr[it][2] * qv[2] + kr[it][3] * qv[3];
+#pragma unroll
+            for (int sh = 1; sh < LPR; sh <<= 1) d += __shfl_xor(d, sh, WAVE);
+            sc[it] = j < j1 ? d * c2 : -INFINITY;
+            pm = fmaxf(pm, sc[it]);
+        }
+        pm = wave_max(pm);
+        const float nm = fmaxf(mx, pm);        // finite: the pass holds at least one key
+        const float corr = exp2f(mx - nm);     // 0 on the first pass (mx = -inf)
+        ls *= corr;
+        o *= corr;
+#pragma unroll
+        for (int it = 0; it < NIT; it++) {
+            const float e = exp2f(sc[it] - nm);   // 0 for rows past the wave's keys
+            ls += e;
+            o += e * vr[it];
+        }
+        mx = nm;
+    }
+    // the wave's sum counts each key row once (lane c4 == 0 of its group),
+    // its O adds the RPI row groups
+    float lrow = c4 == 0 ? ls : 0.f;
+    lrow = wave_sum(lrow);
+#pragma unroll
+    for (int sh = LPR; sh < 64; sh <<= 1) {
+        o[0] += __shfl_xor(o[0], sh, WAVE);
+        o[1] += __shfl_xor(o[1], sh, WAVE);
+        o[2] += __shfl_xor(o[2], sh, WAVE);
+        o[3] += __shfl_xor(o[3], sh, WAVE);
+    }
+    if (sub == 0) wo[wave][c4] = o;
+    if (lane == 0) { wm[wave] = mx; wl[wave] = lrow; }
+    __syncthreads();
+    if (threadIdx.x < LPR) {
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) M = fmaxf(M, wm[w]);
+        float L = 0.f;
+        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < WAVES; w++) {
+            const float wt = wm[w] == -INFINITY ? 0.f : exp2f(wm[w] - M);   // waves without keys weigh 0
+            L += wt * wl[w];
+            acc += wt * wo[w][threadIdx.x];
+        }
+        *(f32x4_t*)(att + (long long)b * D + h * HD + 4 * threadIdx.x) = acc / L;
+    }
+}
+
+#define DEC_ATTN_KERNEL(HD)                                                                                   \
+    extern "C" __global__ void __launch_bounds__(64 * DEC_ATT_WAVES)                                          \
+    k_dec_attn_hd##HD(const float* q, int ldq, const float* kc, const float* vc, const int* pos_dev, int ctx, \
+                      int H, float scale, float* att, int D) {                                                \
+        dec_attn<HD>(q, ldq, kc, vc, pos_dev, ctx, H, scale, att, D);                                         \
+    }
+DEC_ATTN_KERNEL(16)
+DEC_ATTN_KERNEL(32)
+DEC_ATTN_KERNEL(64)
+
+// Lane layout of v_mfma_f32_16x16x4f32 (checked exactly by a test):
+// out[lane*4 + r] = result register r of lane `lane`.
+extern "C" __global__ void k_mfma16_layout_probe(const float* a, const float* b, float* out) {
+    const int l = threadIdx.x;
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[l], b[l], acc, 0, 0, 0);
+#pragma unroll
+    for (int r = 0; r < 4; r++) out[l * 4 + r] = acc[r];
+}

@@ -194,19 +194,28 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
 
 // ---------------------------------------------------------------- column sums
 // out[c] (+)= sum over b of partial[b, c] (the RMSNorm weight gradient's
-// per-block partials).  A block covers 64
-// columns; its 4 wavefronts each add a contiguous quarter of the partial
-// rows in order, and the four quarter sums are added in order.  Loads are
-// issued 16 at a time ahead of their (ordered) additions.
+// per-block partials), over the partial rows of row group blockIdx.y
+// (rows [y*group_rows, min(nb, (y+1)*group_rows)) -> row y of out).  A block
+// covers 64 columns; its 4 wavefronts each add a contiguous quarter of the
+// group's rows in order, and the four quarter sums are added in order.
+// Loads are issued 16 at a time ahead of their (ordered) additions.  The
+// host runs it twice -- 16-row groups over many blocks, then the group sums
+// in group order -- so the reduction fills the GPU and keeps a fixed order.
 extern "C" __global__ void __launch_bounds__(256)
-k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __restrict__ out, int accumulate) {
+k_colsum_final(const float* __restrict__ partial, int nb, int cols, float* __restrict__ out, int accumulate,
+               int group_rows) {
     __shared__ float red[4][64];
     const int cl = threadIdx.x & 63, q = threadIdx.x >> 6;
     const int c = blockIdx.x * 64 + cl;
-    const int per = (nb + 3) / 4;
+    const int g0 = blockIdx.y * group_rows;
+    int gn = nb - g0;
+    if (gn > group_rows) gn = group_rows;
+    partial += (long long)g0 * cols;
+    out += (long long)blockIdx.y * cols;
+    const int per = (gn + 3) / 4;
     const int b0 = q * per;
     int b1 = b0 + per;
-    if (b1 > nb) b1 = nb;
+    if (b1 > gn) b1 = gn;
     float s = 0.f;
     if (c < cols) {
         const float* src = partial + c;

@@ -5,3 +5,4 @@
 #include "rowops.hip"
 #include "attention.hip"
 #include "decode.hip"
+#include "decode_fused.hip"
