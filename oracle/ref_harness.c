@@ -144,7 +144,7 @@ typedef struct RefCfg { u32 V, D, H, L, F; f32 eps; } RefCfg;
 static u64 arena_for(const RefCfg* c, u32 T) {
     u64 per = (u64)T * T * c->H * 48ull + (u64)T * c->V * 24ull + (u64)T * c->D * 400ull * c->L
             + (u64)c->V * c->D * 16ull + (u64)c->L * c->D * c->F * 64ull + (1ull << 30);
-    return per;
+    return 2 * per;   /* a reservation: pages are committed only as the arena is used */
 }
 
 void refh_lm_init(const RefCfg* c, u64 sa, u64 sb, f32* params_out) {

@@ -262,6 +262,17 @@ def test_sample_batch_matches_compiled_reference(orc):
         assert np.array_equal(got[0], want[0]) and np.array_equal(got[1], want[1]), (T, n, B, seed)
 
 
+def test_t1024_fixture_inputs(orc):
+    """The T=1024 fixture's inputs are what the oracle builds: lm_init bits of
+    the real model and the sampler's windows of the 200,000-token stream."""
+    fx = np.load(os.path.join(GOLDEN, "ref_real_t1024.npz"))
+    model = orc.Model(31769, 384, 6, 12, 1024)
+    assert sha(model.init(1337, 1)) == str(fx["params_sha256"])
+    ids, tgt = orc.sample_batch(orc.random_tokens(200000, 31769), 1024, 2, 2026)
+    assert np.array_equal(ids, fx["ids"]) and np.array_equal(tgt, fx["tgt"])
+    assert fx["grad_idx"].shape == (model.num_params, 256)
+
+
 def test_argmax_rule(orc):
     """or_argmax follows the reference's max scan (generate.c:57-58: best
     from index 0, moved only by a strictly greater value): on NaN-free rows
