@@ -437,6 +437,156 @@ def traffic_probe(trlm):
     dev.close()
 
 
+def counter_probe(trlm, phase):
+    """Dispatches for the per-kernel counter tables (profiles/
+    kernel_counters_*.txt): three calibration copies of PROBE_COPY_BYTES,
+    then
+      train:  config 4 with every side section on the main stream
+              (hip_side_serial: no contention between overlapped kernels) --
+              two training steps (forward, CE, backward, AdamW) and one
+              forward;
+      decode: config 5's step kernels at context ~1000 -- a 1000-token
+              prefill of 64 sequences and 4 eager decode steps."""
+    host, hip = trlm.libs()
+    rt = C.CDLL("libamdhip64.so")
+    rt.hipMemcpyDtoD.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
+    dev = trlm.Device()
+    src, dst = dev.empty(PROBE_COPY_BYTES), dev.empty(PROBE_COPY_BYTES)
+    dev.sync()
+    for _ in range(3):
+        assert rt.hipMemcpyDtoD(dst, src, PROBE_COPY_BYTES) == 0
+    dev.sync()
+    dev.free(src)
+    dev.free(dst)
+    dev.close()
+    rng = np.random.default_rng(7)
+    params = model_params(rng)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    try:
+        if phase == "train":
+            tr = trlm.Trainer(hm, B, T)
+            adam = trlm.Adam(hm, 3e-4, 0.9, 0.95, 1e-8)
+            ids = rng.integers(0, V, M, dtype=np.uint32)
+            tgt = rng.integers(0, V, M, dtype=np.uint32)
+            hip.hip_side_serial(1)
+            try:
+                for _ in range(2):
+                    tr.forward_backward(ids, tgt)
+                    tr.adamw_step(adam, 0.1)
+                tr.eval_loss(ids, tgt)
+                hip.hip_sync()
+            finally:
+                hip.hip_side_serial(0)
+                tr.destroy()
+        else:
+            os.environ["TRLM_DECODE_EAGER"] = "1"   # kernel tracers cannot follow graph replays here
+            tr = trlm.Trainer(hm, 1, 8)
+            dec = trlm.Decoder(tr, DEC_B, DEC_CTX)
+            try:
+                prompt = rng.integers(0, V, DEC_B * 1000, dtype=np.uint32).reshape(DEC_B, 1000)
+                dec.generate_greedy(prompt, 5)
+            finally:
+                dec.destroy()
+                tr.destroy()
+    finally:
+        hm.close()
+    print("counter probe (%s) done" % phase, flush=True)
+
+
+TILE_DIMS = {"256x128": (256, 128), "128x256": (128, 256), "128x128": (128, 128), "128x128_k32": (128, 128),
+             "64x128": (64, 128), "64x128_k32": (64, 128), "64x64": (64, 64), "64x64_k32": (64, 64)}
+
+
+def gemm_roles():
+    """(kernel, total work-items) -> role for the B8 T1024 training step's
+    GEMMs (and their split-K reductions), from the engine's own plan
+    (trlm_gemm_plan); launches are tiles x 256 work-items x splits."""
+    _, hip = load_trlm().libs()
+    shapes = [("QKV fwd", 0, 0, M, 3 * D, D), ("attn-out fwd", 0, 0, M, D, D), ("gate_up fwd", 0, 0, M, 2 * F, D),
+              ("down fwd", 0, 0, M, D, F), ("LM-head fwd", 0, 1, M, V, D), ("QKV dX", 0, 1, M, D, 3 * D),
+              ("attn-out dX", 0, 1, M, D, D), ("gate_up dX", 0, 1, M, D, 2 * F), ("down dX", 0, 1, M, F, D),
+              ("LM-head dX", 0, 0, M, D, V), ("QKV dW", 1, 0, D, 3 * D, M), ("attn-out dW", 1, 0, D, D, M),
+              ("gate_up dW", 1, 0, D, 2 * F, M), ("down dW", 1, 0, F, D, M), ("LM-head dW", 1, 0, V, D, M)]
+    roles = {}
+    sp = C.c_int32()
+    for role, ta, tb, m, n, k in shapes:
+        name = hip.trlm_gemm_plan(ta, tb, m, n, k, 1, C.byref(sp)).decode()
+        bm, bn = TILE_DIMS[name.split("_", 3)[3]]
+        splits = sp.value if role not in ("QKV fwd", "LM-head fwd") else 1   # RoPE / row statistics: no split
+        grid = -(-m // bm) * -(-n // bn) * 256 * splits
+        roles.setdefault((name[:40], str(grid)), []).append(role)
+        if splits > 1:
+            for rows in (m, m + 1):   # the weight gradients' partials carry the bias sums in an extra row
+                g2 = -(-(rows * n) // 256) * 256
+                roles.setdefault(("k_gemm_splitk_reduce", str(g2)), []).append(role + " reduce")
+    attn_grid = B * H * -(-T // 64) * 256
+    for k in ("k_attn_fwd_hd64", "k_attn_bwd_dkv_hd64", "k_attn_bwd_dq_hd64"):
+        roles[(k, str(attn_grid))] = ["B8 T1024"]
+    return {k: " / ".join(sorted(set(v))) for k, v in roles.items()}
+
+
+def counter_summary(phase, trace_dir, busy_dir, fetch_dir, write_dir):
+    """Per-kernel table from a --kernel-trace run and three --pmc runs of
+    --counter-probe PHASE: average duration; matrix-core use = SQ_VALU_MFMA_
+    BUSY_CYCLES / (1024 SIMDs x kernel cycles), kernel cycles = SQ_CYCLES /
+    32 shader engines; HBM bytes = FETCH_SIZE and WRITE_SIZE scaled by the
+    factors that make the calibration copies read their true size, and the
+    GB/s they give over the kernel's average duration.  The decode table
+    lists the step's kernels only (not the prefill's)."""
+    import csv
+    import glob
+
+    def rows(d, pat):
+        for f in glob.glob(os.path.join(d, "**", pat), recursive=True):
+            with open(f) as fh:
+                for r in csv.DictReader(fh):
+                    yield r
+
+    def key(r):
+        if "Grid_Size_X" in r:   # kernel trace: per dimension
+            grid = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        else:                    # counter collection: total work-items
+            grid = int(r["Grid_Size"])
+        return (r["Kernel_Name"][:40], str(grid))
+
+    dur = {}
+    for r in rows(trace_dir, "*kernel_trace.csv"):
+        dur.setdefault(key(r), []).append(int(r["End_Timestamp"]) - int(r["Start_Timestamp"]))
+    ctr = {}
+    for d in (busy_dir, fetch_dir, write_dir):
+        per = {}
+        for r in rows(d, "*counter_collection.csv"):
+            k = (key(r), r["Dispatch_Id"], r["Counter_Name"])
+            per[k] = per.get(k, 0.0) + float(r["Counter_Value"])
+        for (k, _, c), v in per.items():
+            ctr.setdefault(k, {}).setdefault(c, []).append(v)
+    # the calibration copies: the copyBuffer dispatches of the largest grid
+    # (the others are small staging copies of host uploads)
+    copies = [k for k in ctr if "copyBuffer" in k[0]]
+    copy = [k for k in copies if int(k[1]) == max(int(c[1]) for c in copies)]
+    kib = PROBE_COPY_BYTES / 1024.0
+    f_fetch = kib / np.median([v for k in copy for v in ctr[k].get("FETCH_SIZE", [])])
+    f_write = kib / np.median([v for k in copy for v in ctr[k].get("WRITE_SIZE", [])])
+    roles = gemm_roles() if phase == "train" else {}
+    print("calibration: copies of %d B; FETCH_SIZE x %.4f, WRITE_SIZE x %.4f" % (PROBE_COPY_BYTES, f_fetch, f_write))
+    print("%-24s %-22s %9s %6s %9s %7s %9s %9s %8s %6s" % ("kernel", "role", "grid", "calls", "avg_us", "mfma%",
+                                                          "fetch_MB", "write_MB", "GB/s", "%HBM"))
+    for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
+        if k not in ctr or "copyBuffer" in k[0]:
+            continue
+        if phase == "decode" and not (k[0].startswith("k_dec_") or k[0].startswith("k_argmax")):
+            continue
+        c = {n: float(np.median(x)) for n, x in ctr[k].items()}
+        avg = sum(v) / len(v) / 1e3
+        busy = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (32.0 * c["SQ_CYCLES"]) if c.get("SQ_CYCLES") else float("nan")
+        fb = c.get("FETCH_SIZE", float("nan")) * 1024.0 * f_fetch / 1e6
+        wb = c.get("WRITE_SIZE", float("nan")) * 1024.0 * f_write / 1e6
+        gbs = (fb + wb) / avg * 1e3   # MB per us -> GB/s
+        print("%-24s %-22s %9s %6d %9.2f %6.1f%% %9.2f %9.2f %8.0f %5.1f%%" % (
+            k[0].replace("k_gemm_", "gemm_")[:24], roles.get(k, "")[:22], k[1], len(v), avg, 100.0 * busy, fb, wb,
+            gbs, 100.0 * gbs / 8000.0))
+
+
 def traffic_summarize(fetch_dir, write_dir):
     """FETCH_SIZE / WRITE_SIZE (KiB per dispatch) of the probe's copies and
     LM-head GEMMs; each counter is scaled by the factor that makes it read
@@ -485,6 +635,9 @@ def traffic_bytes():
 
 
 def main():
+    if len(sys.argv) > 6 and sys.argv[1] == "--counter-summary":
+        counter_summary(*sys.argv[2:7])
+        return
     if len(sys.argv) > 3 and sys.argv[1] == "--traffic-summarize":
         traffic_summarize(sys.argv[2], sys.argv[3])
         return
@@ -509,6 +662,9 @@ def main():
     ap.add_argument("--decode-only", action="store_true", help="only the config-5 decode measurement (JSON line)")
     ap.add_argument("--traffic-probe", action="store_true",
                     help="only the dispatches the FETCH_SIZE / WRITE_SIZE counter passes read")
+    ap.add_argument("--counter-probe", choices=["train", "decode"], default=None,
+                    help="the dispatches of a per-kernel counter table: calibration copies, then config 4 with "
+                         "the side stream serialised (train) or config-5 decode steps at context ~1000 (decode)")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
@@ -525,6 +681,9 @@ def main():
         return
     if args.traffic_probe:
         traffic_probe(trlm)
+        return
+    if args.counter_probe:
+        counter_probe(trlm, args.counter_probe)
         return
     if args.model_only:
         print(json.dumps(model_benchmarks(trlm, args.steps, max(6, args.warmup))), flush=True)
