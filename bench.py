@@ -17,13 +17,15 @@ roofline: the LM-head forward GEMM (the largest single kernel), algorithmic
 with HIP events on the library's stream.
 
 cpu_baseline: the reference's own CPU matmul (tensor_matmul2d, built from
-/root/reference into oracle/_ref) on a bounded sample of the sweep; falls
-back to the oracle restatement when oracle/_ref was not built.
-cpu_train: the reference's CPU training step on the host cores (one thread
-per sequence running lm_forward + backward, the gradient average, then
-adam_step_parallel, as training/data_parallel.c and training/adam.c run it)
-on a bounded sample (the real 12-layer model, one T=32 sequence per
-thread), as tokens/s beside the GPU's config-4 rate.
+/root/reference into oracle/_ref) on the sweep's whole QKV forward GEMM, its
+rows split over 8 host threads; falls back to the oracle restatement when
+oracle/_ref was not built.
+cpu_model: the reference's CPU forward (config 3) and training step
+(config 4) at B=8, T=1024 on 8 host threads, one sequence each, as
+training/data_parallel.c runs it, from one transformer block at T=1024 and
+16 rows of the head timed at that shape and scaled to the 12 layers and
+1024 rows (cpu_model_baseline); gpu_vs_cpu_forward / gpu_vs_cpu_train are
+the GPU's rates over these.
 """
 import argparse
 import ctypes as C
@@ -279,63 +281,90 @@ def decode_benchmark(trlm):
                 DEC_B, DEC_PROMPT, DEC_CTX, steps - 1)}
 
 
-def cpu_baseline(seconds_target=10.0):
-    """Reference tensor_matmul2d (or the oracle) on QKV-shaped rows."""
+CPU_THREADS = 8        # one per sequence of the B=8 batch, as data_parallel_step runs it
+CPU_HEAD_ROWS = 16     # rows of the timed head piece; every head row costs the same
+
+
+def host_cpu():
+    """nproc, the cores this process may run on, and the CPU model name."""
+    model = "?"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                if ln.startswith("model name"):
+                    model = ln.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"nproc": os.cpu_count(), "affinity": len(os.sched_getaffinity(0)), "model": model}
+
+
+def cpu_baseline():
+    """The reference's tensor_matmul2d on the whole QKV forward GEMM of the
+    sweep (8192x1152x384), its rows split over CPU_THREADS concurrent threads,
+    each running the reference's single-threaded loop on its share (the
+    reference parallelises over sequences, one thread each); the oracle's
+    reference-order matmul on one thread when oracle/_ref was not built."""
     import oracle
     rng = np.random.default_rng(1)
     K, N = D, 3 * D
     Wq = (0.02 * rng.standard_normal((K, N))).astype(np.float32)
-    kind = "reference" if oracle.reference_available() else "port"
-    rows = 64
-    while True:
-        X = rng.standard_normal((rows, K)).astype(np.float32)
-        out = np.zeros((rows, N), np.float32)
-        if kind == "reference":
-            ref = oracle.Reference()
-            dt = ref.h.refh_time_matmul(rows, N, K, X, Wq, out)
-        else:
-            t0 = time.perf_counter()
-            oracle.matmul(X, Wq)
-            dt = time.perf_counter() - t0
-        if dt * 2 >= seconds_target or rows >= M:
-            break
-        rows = min(M, int(rows * max(2.0, seconds_target / max(dt, 1e-3) * 0.6)))
-    tflops = 2.0 * rows * N * K / dt / 1e12
-    return {"value": tflops, "unit": "TFLOP/s", "cores": 1, "kind": kind,
-            "sample": "QKV forward GEMM rows 0..%d (%dx%dx%d) through %s, %.1f s" % (
-                rows - 1, rows, N, K, "tensor_matmul2d (oracle/_ref)" if kind == "reference"
-                else "the oracle's reference-order matmul", dt)}
-
-
-def cpu_train_baseline(T=32):
-    """The reference's CPU training step (oracle/_ref; the oracle's port
-    otherwise) on the real architecture, one sequence of T tokens per host
-    thread, timed once."""
-    import oracle
-    threads = max(1, min(16, os.cpu_count() or 1))
-    model = oracle.Model(V, D, H, L, F)
-    tok = oracle.random_tokens(4 * threads * T + T + 2, V)
-    ids, tgt = oracle.sample_batch(tok, T, threads, 2026)
+    X = rng.standard_normal((M, K)).astype(np.float32)
     if oracle.reference_available():
-        ref = oracle.Reference()
-        params = ref.lm_init(model)
-        grads = np.zeros(model.total, np.float32)
-        scratch = np.zeros(model.total * threads, np.float32)
-        run = lambda b: ref.h.refh_time_train_step(C.byref(model.cfg), params, ids, tgt, b, T, model.total,
-                                                   grads, scratch, threads)
-        kind = "reference"
+        out = np.zeros((M, N), np.float32)
+        dt = oracle.Reference().h.refh_time_matmul_threads(M, N, K, X, Wq, out, CPU_THREADS)
+        rows, cores, kind = M, CPU_THREADS, "reference"
+        what = "tensor_matmul2d (oracle/_ref), rows split over %d threads" % cores
     else:
-        params = model.init(1337, 1)
+        rows, cores, kind = 512, 1, "port"
+        t0 = time.perf_counter()
+        oracle.matmul(X[:rows], Wq)
+        dt = time.perf_counter() - t0
+        what = "the oracle's reference-order matmul, 1 thread"
+    tflops = 2.0 * rows * N * K / dt / 1e12
+    return {"value": tflops, "unit": "TFLOP/s", "cores": cores, "kind": kind,
+            "sample": "QKV forward GEMM %dx%dx%d through %s, %.1f s" % (rows, N, K, what, dt)}
 
-        def run(b):
-            t0 = time.perf_counter()
-            model.forward_backward(params, ids[:b * T], tgt[:b * T], b, T)
-            return time.perf_counter() - t0
-        kind = "port"
-    dt = run(threads)
-    return {"tokens_per_s": threads * T / dt, "threads": threads, "kind": kind,
-            "sample": "%d sequences x T=%d of the 12-layer d=384 model, one per thread: forward, backward, "
-                      "gradient average, adam_step_parallel; %.1f s" % (threads, T, dt)}
+
+def cpu_model_baseline():
+    """Config 3 (forward + CE) and config 4 (training step) of the
+    reference's CPU path at B=8, T=1024, from pieces timed at that shape
+    (oracle/ref_harness.c refh_time_pieces): CPU_THREADS concurrent threads,
+    one sequence each, run one transformer_block over T=1024 rows (forward,
+    then backward) and the embedding + final RMSNorm + tied head + CE over
+    CPU_HEAD_ROWS rows (forward, then backward); adam_step_parallel is timed
+    over the whole model.  A step is then 12 * block + (T / rows) * head
+    (+ Adam), since the 12 blocks are identical and a head row's cost does
+    not depend on T.  Needs oracle/_ref (None without it)."""
+    import oracle
+    if not oracle.reference_available():
+        return None
+    ref = oracle.Reference()
+    model = oracle.Model(V, D, H, L, F)
+    params = ref.lm_init(model)
+    tok = oracle.random_tokens(4 * CPU_THREADS * T + T + 2, V)
+    ids, tgt = oracle.sample_batch(tok, T, CPU_THREADS, 2026)
+    out = np.zeros(4)
+    t0 = time.perf_counter()
+    rc = ref.h.refh_time_pieces(C.byref(model.cfg), params, ids, tgt, T, CPU_HEAD_ROWS, CPU_THREADS, out)
+    if rc != 0:
+        raise RuntimeError("refh_time_pieces failed: %d" % rc)
+    grads = (1e-3 * np.random.default_rng(3).standard_normal(model.total)).astype(np.float32)
+    adam = ref.h.refh_time_adam(C.byref(model.cfg), params.copy(), grads, CPU_THREADS)
+    wall = time.perf_counter() - t0
+    scale = T / CPU_HEAD_ROWS
+    fwd_s = L * out[0] + scale * out[2]
+    step_s = L * out[1] + scale * out[3] + adam
+    tokens = CPU_THREADS * T
+    return {"fwd_tokens_per_s": tokens / fwd_s, "train_tokens_per_s": tokens / step_s,
+            "fwd_s": fwd_s, "step_s": step_s, "threads": CPU_THREADS, "kind": "reference",
+            "pieces_s": {"block_fwd": out[0], "block_fwd_bwd": out[1], "head_fwd": out[2],
+                         "head_fwd_bwd": out[3], "adam": adam},
+            "sample": ("reference CPU path (oracle/_ref), %d threads, one T=%d sequence each: one transformer_block "
+                       "fwd / fwd+bwd at T=%d and embedding+final norm+tied head+CE fwd / fwd+bwd on %d rows, "
+                       "timed together; step = %d x block + %d x head (+ adam_step_parallel over all %d "
+                       "parameters); %.0f s of wall" % (CPU_THREADS, T, T, CPU_HEAD_ROWS, L, int(scale),
+                                                        model.total, wall))}
 
 
 def summarize_profile(path):
@@ -737,18 +766,23 @@ def main():
         log("decode: config 5")
         line.update({k: (round(v, 3) if isinstance(v, float) else v) for k, v in decode_benchmark(trlm).items()})
     if not args.no_cpu:
-        log("cpu baseline leg")
+        log("cpu baseline leg: QKV GEMM through the reference's tensor_matmul2d")
         cb = cpu_baseline()
         line["cpu_baseline"] = {"value": cb["value"], "unit": cb["unit"], "cores": cb["cores"], "kind": cb["kind"],
                                 "sample": cb["sample"]}
+        line["cpu_host"] = host_cpu()
         line["gpu_vs_cpu_gemm"] = round(value / cb["value"], 1)
         if not args.no_model:
-            log("cpu baseline: reference training step on the host cores")
-            ct = cpu_train_baseline()
-            line["cpu_train"] = {"tokens_per_s": round(ct["tokens_per_s"], 2), "threads": ct["threads"],
-                                 "kind": ct["kind"], "sample": ct["sample"]}
-            if "train_tokens_per_s" in line:
-                line["gpu_vs_cpu_train"] = round(line["train_tokens_per_s"] / ct["tokens_per_s"], 1)
+            log("cpu baseline: the reference's forward and training step at B=8 T=1024 (about 70 s)")
+            ct = cpu_model_baseline()
+            if ct is not None:
+                line["cpu_model"] = {k: (round(v, 3) if isinstance(v, float) else v) for k, v in ct.items()
+                                     if k != "pieces_s"}
+                line["cpu_model"]["pieces_s"] = {k: round(v, 3) for k, v in ct["pieces_s"].items()}
+                if "fwd_tokens_per_s" in line:
+                    line["gpu_vs_cpu_forward"] = round(line["fwd_tokens_per_s"] / ct["fwd_tokens_per_s"], 1)
+                if "train_tokens_per_s" in line:
+                    line["gpu_vs_cpu_train"] = round(line["train_tokens_per_s"] / ct["train_tokens_per_s"], 1)
     print(json.dumps(line), flush=True)
 
 

@@ -336,6 +336,12 @@ class Reference:
         h.refh_checkpoint_load.argtypes = [C.POINTER(RefCfg), C.c_char_p, f32p, C.c_void_p, C.c_void_p,
                                            C.POINTER(C.c_uint64), C.c_int]
         h.refh_time_matmul.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p]
+        h.refh_time_matmul_threads.restype = C.c_double
+        h.refh_time_matmul_threads.argtypes = [C.c_uint32, C.c_uint32, C.c_uint32, f32p, f32p, f32p, C.c_int]
+        h.refh_time_pieces.restype = C.c_int
+        h.refh_time_pieces.argtypes = [cfgp, f32p, u32p, u32p, C.c_uint32, C.c_uint32, C.c_int, f64p]
+        h.refh_time_adam.restype = C.c_double
+        h.refh_time_adam.argtypes = [cfgp, f32p, f32p, C.c_int]
 
     def lm_init(self, model, seed_a=1337, seed_b=1):
         p = np.zeros(model.total, np.float32)

@@ -27,6 +27,9 @@
 #include "tensor/tensor.h"
 #include "autograd/node.h"
 #include "model/lm_model.h"
+#include "model/transformer_block.h"
+#include "model/embedding.h"
+#include "model/model_ops.h"
 #include "model/attention.h"
 #include "model/rope.h"
 #include "model/loss.h"
@@ -61,6 +64,12 @@ static struct {
     bool32 (*checkpoint_load)(Allocator*, const char*, Node**, u32, AdamOptimizer*);
     f32 (*lr_warmup_cosine)(u64, u64, u64, f32, f32);
     void (*gpu_trainer_sample_batch)(const u32*, u64, u32, u32, u64, u32*, u32*);
+    Node* (*transformer_block)(Allocator*, Node*, const BlockWeights*, u32, u32, u64, Node*, Node*, Node*, f32, i32);
+    Node* (*node_embedding_lookup)(Allocator*, Node*, const u32*, u64);
+    Node* (*node_rmsnorm)(Allocator*, Node*, Node*, f32);
+    Node* (*node_transpose)(Allocator*, Node*, u32, u32);
+    Node* (*node_matmul2d)(Allocator*, Node*, Node*);
+    Node* (*node_sum_all)(Allocator*, Node*);
     int ok;
 } R;
 
@@ -80,6 +89,8 @@ int refh_open(const char* lib_path) {
     LOAD(checkpoint_save); LOAD(checkpoint_load);
     LOAD(lr_warmup_cosine);
     LOAD(gpu_trainer_sample_batch);
+    LOAD(transformer_block); LOAD(node_embedding_lookup); LOAD(node_rmsnorm);
+    LOAD(node_transpose); LOAD(node_matmul2d); LOAD(node_sum_all);
     R.ok = 1;
     return 0;
 }
@@ -346,6 +357,146 @@ double refh_time_train_step(const RefCfg* c, f32* params, const u32* ids, const 
 double refh_time_forward(const RefCfg* c, const f32* params, const u32* ids, u32 B, u32 T, f32* logits, int nthreads) {
     double t0 = now_s();
     refh_forward_logits(c, params, ids, B, T, logits, nthreads);
+    return now_s() - t0;
+}
+
+/* ---- the reference's CPU step in pieces, for a bounded baseline ----
+ *
+ * A full B=8, T=1024 step of the 12-layer model takes minutes on the host
+ * cores, so the timed sample is its two kinds of piece, each run by
+ * nthreads concurrent threads (one sequence each, as data_parallel_step
+ * gives every sequence a thread), all released together by a barrier:
+ *   block: one transformer_block (model/transformer_block.c) over T rows,
+ *          forward, then node_sum_all + backward (gradients of the block's
+ *          weights and of its input, as inside the full model);
+ *   head:  node_embedding_lookup over R rows, the final node_rmsnorm, the
+ *          tied node_matmul2d against node_transpose(embed_table), and
+ *          node_cross_entropy_loss (model/lm_model.c:62-82), forward then
+ *          backward.
+ * Every row of the head piece costs the same whatever T is (no attention),
+ * so a step is  L * block(T) + (T / R) * head(R)  plus the optimizer.
+ * out[0] / out[1]: block forward / forward+backward wall seconds;
+ * out[2] / out[3]: head forward / forward+backward wall seconds.  Wall =
+ * latest finish minus earliest start over the threads. */
+typedef struct PieceWork {
+    const RefCfg* c; const f32* params; const u32* ids; const u32* tgt; u32 T, R;
+    pthread_barrier_t* bar;
+    double t0[2], t1[2], t2[2];
+} PieceWork;
+
+static void* piece_run(void* arg) {
+    PieceWork* w = (PieceWork*)arg;
+    const RefCfg* c = w->c;
+    Allocator a = R.allocator_create(arena_for(c, w->T));
+    Node* ps[LM_MAX_LAYERS * 12 + 2];
+    u32 np;
+    LMModel m = model_from_flat(&a, c, w->params, ps, &np);
+    u32 hd = c->D / c->H;
+    u64 cs[2] = { w->T, hd / 2 }, ms[2] = { w->T, w->T }, xs[2] = { w->T, c->D };
+    Tensor ct = R.tensor_create(&a, cs, 2), st = R.tensor_create(&a, cs, 2), mt = R.tensor_create(&a, ms, 2);
+    R.rope_build_tables(&ct, &st, w->T, hd, 10000.0f);
+    R.build_causal_mask(&mt);
+    Node* cl = R.node_leaf(&a, ct, FALSE);
+    Node* sl = R.node_leaf(&a, st, FALSE);
+    Node* ml = R.node_leaf(&a, mt, FALSE);
+    Tensor xt = R.tensor_create(&a, xs, 2);   /* the block's input: the sequence's embedding rows */
+    for (u32 t = 0; t < w->T; t++)
+        memcpy(xt.data + (u64)t * c->D, w->params + (u64)w->ids[t] * c->D, c->D * sizeof(f32));
+    Node* x = R.node_leaf(&a, xt, TRUE);
+
+    pthread_barrier_wait(w->bar);
+    w->t0[0] = now_s();
+    Node* y = R.transformer_block(&a, x, &m.blocks[0], c->H, 1, w->T, cl, sl, ml, m.eps, 0);
+    Node* s = R.node_sum_all(&a, y);
+    w->t1[0] = now_s();
+    R.backward(&a, s);
+    w->t2[0] = now_s();
+
+    pthread_barrier_wait(w->bar);
+    w->t0[1] = now_s();
+    Node* e = R.node_embedding_lookup(&a, m.embed_table, w->ids, w->R);
+    Node* h = R.node_rmsnorm(&a, e, m.final_norm_w, m.eps);
+    Node* et = R.node_transpose(&a, m.embed_table, 0, 1);
+    Node* lg = R.node_matmul2d(&a, h, et);
+    Node* loss = R.node_cross_entropy_loss(&a, lg, w->tgt);
+    w->t1[1] = now_s();
+    R.backward(&a, loss);
+    w->t2[1] = now_s();
+    R.allocator_destroy(&a);
+    return NULL;
+}
+
+int refh_time_pieces(const RefCfg* c, const f32* params, const u32* ids, const u32* tgt, u32 T, u32 R_rows,
+                     int nthreads, double* out) {
+    if (nthreads < 1 || nthreads > 64 || R_rows < 1 || R_rows > T || c->L < 1) return -1;
+    PieceWork ws[64];
+    pthread_t th[64];
+    pthread_barrier_t bar;
+    pthread_barrier_init(&bar, NULL, (unsigned)nthreads);
+    for (int w = 0; w < nthreads; w++) {
+        memset(&ws[w], 0, sizeof(PieceWork));
+        ws[w].c = c; ws[w].params = params; ws[w].ids = ids + (u64)w * T; ws[w].tgt = tgt + (u64)w * T;
+        ws[w].T = T; ws[w].R = R_rows; ws[w].bar = &bar;
+    }
+    for (int w = 0; w < nthreads; w++) pthread_create(&th[w], NULL, piece_run, &ws[w]);
+    for (int w = 0; w < nthreads; w++) pthread_join(th[w], NULL);
+    pthread_barrier_destroy(&bar);
+    for (int k = 0; k < 2; k++) {
+        double s0 = ws[0].t0[k], e1 = ws[0].t1[k], e2 = ws[0].t2[k];
+        for (int w = 1; w < nthreads; w++) {
+            if (ws[w].t0[k] < s0) s0 = ws[w].t0[k];
+            if (ws[w].t1[k] > e1) e1 = ws[w].t1[k];
+            if (ws[w].t2[k] > e2) e2 = ws[w].t2[k];
+        }
+        out[2 * k] = e1 - s0;
+        out[2 * k + 1] = e2 - s0;
+    }
+    return 0;
+}
+
+/* Wall seconds of adam_step_parallel (training/adam.c:70-102) over the whole
+ * model's parameters with the gradients given, on nthreads threads. */
+double refh_time_adam(const RefCfg* c, f32* params, const f32* grads, int nthreads) {
+    Allocator a = R.allocator_create(arena_for(c, 1));
+    Node* ps[LM_MAX_LAYERS * 12 + 2];
+    u32 np;
+    model_from_flat(&a, c, params, ps, &np);
+    AdamOptimizer opt = R.adam_create(&a, ps, np, 3e-4f, 0.9f, 0.95f, 1e-8f);
+    u64 off = 0;
+    for (u32 i = 0; i < np; i++) { memcpy(ps[i]->grad.data, grads + off, ps[i]->grad.numel * 4); off += ps[i]->grad.numel; }
+    double t0 = now_s();
+    R.adam_step_parallel(&opt, (u32)nthreads);
+    double t1 = now_s();
+    R.allocator_destroy(&a);
+    return t1 - t0;
+}
+
+/* Wall seconds of an M x N x K product through tensor_matmul2d
+ * (tensor/tensor.c:351-373) split by rows over nthreads concurrent threads,
+ * each running the reference's single-threaded loop on its own rows. */
+typedef struct MmWork { u32 M, N, K; const f32* A; const f32* B; f32* C; } MmWork;
+
+static void* mm_run(void* arg) {
+    MmWork* w = (MmWork*)arg;
+    if (w->M) refh_matmul(w->M, w->N, w->K, w->A, w->B, w->C);
+    return NULL;
+}
+
+double refh_time_matmul_threads(u32 M, u32 N, u32 K, const f32* A, const f32* B, f32* C, int nthreads) {
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > 64) nthreads = 64;
+    MmWork ws[64];
+    pthread_t th[64];
+    u32 per = (M + (u32)nthreads - 1) / (u32)nthreads;
+    double t0 = now_s();
+    for (int w = 0; w < nthreads; w++) {
+        u32 r0 = (u32)w * per < M ? (u32)w * per : M;
+        u32 r1 = r0 + per < M ? r0 + per : M;
+        ws[w].M = r1 - r0; ws[w].N = N; ws[w].K = K;
+        ws[w].A = A + (u64)r0 * K; ws[w].B = B; ws[w].C = C + (u64)r0 * N;
+        pthread_create(&th[w], NULL, mm_run, &ws[w]);
+    }
+    for (int w = 0; w < nthreads; w++) pthread_join(th[w], NULL);
     return now_s() - t0;
 }
 
