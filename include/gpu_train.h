@@ -88,6 +88,7 @@ typedef struct GpuTrainer {
     f32* host_norm_partial;
     hipDeviceptr_t ce_stats;                  /* [N][ce_stats_cap] (max, sum) from the LM-head GEMM */
     i32 ce_stats_cap, ce_nst;
+    hipDeviceptr_t ce_zt;                     /* [N] each row's target logit (eval: logits not stored) */
 } GpuTrainer;
 
 GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,

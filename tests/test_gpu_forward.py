@@ -73,6 +73,34 @@ def test_forward_loss_keeps_logits(trlm, orc, V, D, H, L, F, T, B):
     assert np.array_equal(am, host_argmax(logits2))
 
 
+@pytest.mark.parametrize("V,D,H,T,B", [(50, 32, 2, 12, 5), (1001, 32, 2, 64, 3), (31769, 64, 4, 128, 2)])
+def test_eval_loss_without_logits(trlm, orc, V, D, H, T, B):
+    """eval_loss never writes the logits: the LM-head GEMM leaves the row
+    statistics and each row's target logit.  Its loss must equal, bit for
+    bit, the loss forward_loss_logits computes from stored logits, for
+    targets on tile and wave-column edges, the first and the last column."""
+    L, F = 2, 2 * D
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    toks = orc.random_tokens(20000, V)
+    ids, tgt = orc.sample_batch(toks, T, B, 91)
+    edges = [c for c in (0, 1, 31, 32, 63, 64, 65, 127, 128, 255, 256, V - 2, V - 1) if 0 <= c < V]
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, B, T)
+    try:
+        for k, targets in enumerate([tgt, np.zeros_like(tgt), np.full_like(tgt, V - 1),
+                                     np.resize(np.array(edges, np.uint32), tgt.size)]):
+            loss, _ = tr.forward_loss_logits(ids, targets)
+            ev = tr.eval_loss(ids, targets)
+            assert np.float32(loss).view(np.uint32) == np.float32(ev).view(np.uint32), (k, loss, ev)
+        cpu_loss, _, _ = model.forward_backward(params, ids, tgt, B, T, want_grads=False)
+        ev = tr.eval_loss(ids, tgt)
+        assert abs(ev - cpu_loss) <= 1e-4 * abs(cpu_loss)
+    finally:
+        tr.destroy()
+        hm.close()
+
+
 def test_argmax_ties_pick_lowest_index(trlm):
     """Rows with repeated maxima: the kernel must return the first index."""
     _, hip = trlm.libs()

@@ -45,7 +45,11 @@ void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hi
  *          weight gradient); single GEMM, B stored [K,N];
  *   rope:  columns [0, rope_cols) of C rotated as RoPE pairs of heads of
  *          rope_hd columns at position row % rope_T (tables [rope_T][rope_hd/2]),
- *          after bias; single GEMM; no split-K.
+ *          after bias; single GEMM; no split-K;
+ *   tgt / tgt_val (with stats): tgt_val[m] = C[m, tgt[m]], the value the
+ *          epilogue computes for that element (tgt[m] < N);
+ *   no_store (with stats): C is not written -- the statistics (and tgt_val)
+ *          are the whole output.
  * Returns the stats entries written per row (0 without stats). */
 typedef struct TrlmGemmExtra {
     hipDeviceptr_t stats;
@@ -54,6 +58,9 @@ typedef struct TrlmGemmExtra {
     const f32* rope_cos;
     const f32* rope_sin;
     i32 rope_T, rope_hd, rope_cols;
+    hipDeviceptr_t tgt;
+    hipDeviceptr_t tgt_val;
+    i32 no_store;
 } TrlmGemmExtra;
 i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,

@@ -204,6 +204,7 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     hip_memset_zero(g.logits, N * (u64)g.ldv * F4);
     g.ce_stats_cap = 2 * (i32)((g.V + 63) / 64);     /* two entries per 64-wide (smallest) tile column */
     g.ce_stats = dalloc(N * (u64)g.ce_stats_cap * 2);
+    g.ce_zt = dalloc(N);
 
     for (u32 i = 0; i < GPU_TRAIN_DRES_RING; i++) g.dres[i] = dalloc(N * D);
     g.dn = dalloc(N * D);
@@ -459,17 +460,47 @@ static void forward_to_logits(GpuTrainer* g, const u32* ids) {
                              NULL, NULL, ldv, &x);
 }
 
-/* targets NULL: already in g->targets. */
-static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
-    if (targets) {
-        trlm_check_ids(g, targets, "targets");
-        hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
-    }
+/* The evaluation forward (forward + mean CE, no gradient): the LM-head
+ * GEMM's epilogue leaves only what the cross-entropy reads -- each row's
+ * softmax statistics and its target's logit -- and never writes the
+ * [N, V] logits, so the loss needs no logits round trip through HBM
+ * (model/gpu_train.c:378-384 writes them and reads them back).  The
+ * targets must already be on the device. */
+static void forward_to_loss_stats(GpuTrainer* g, const u32* ids) {
+    i32 N = (i32)g->N, D = (i32)g->D, V = (i32)g->V, ldv = (i32)g->ldv;
+    trlm_forward_hidden(g, ids, NULL, NULL);
+    TrlmGemmExtra x;
+    memset(&x, 0, sizeof(x));
+    x.stats = g->ce_stats;
+    x.stats_cap = g->ce_stats_cap;
+    x.tgt = g->targets;
+    x.tgt_val = g->ce_zt;
+    x.no_store = 1;
+    g->ce_nst = trlm_gemm_ex(g->gemm, 0, 1, g->nf, P_(g, 0), g->logits, N, V, D, D, D, ldv, 1, 0, 0, 0, 1.0f, 0.0f,
+                             NULL, NULL, ldv, &x);
+}
+
+static void upload_targets(GpuTrainer* g, const u32* targets) {
+    trlm_check_ids(g, targets, "targets");
+    hip_h2d(g->targets, targets, (u64)g->N * sizeof(u32));
+}
+
+/* targets NULL: already in g->targets.  from_stats: the logits were not
+ * stored (forward_to_loss_stats); the loss comes from the statistics and
+ * the target logits alone, and no gradient is formed. */
+static void cross_entropy_ex(GpuTrainer* g, const u32* targets, i32 write_grad, i32 from_stats) {
+    if (targets) upload_targets(g, targets);
     hipDeviceptr_t lg = g->logits, tg = g->targets, lr = g->loss_rows, st = g->ce_stats;
+    hipDeviceptr_t zt = from_stats ? g->ce_zt : NULL;
     i32 ld = (i32)g->ldv, V = (i32)g->V, nst = g->ce_nst;
     f32 grad_scale = 1.0f / (f32)g->N;
-    void* args[] = { &lg, &ld, &tg, &lr, &V, &grad_scale, &write_grad, &st, &nst };
+    if (from_stats) write_grad = 0;
+    void* args[] = { &lg, &ld, &tg, &lr, &V, &grad_scale, &write_grad, &st, &nst, &zt };
     hip_launch(g->k.cross_entropy, g->N, 1, 1, 256, 1, 1, 0, args);
+}
+
+static void cross_entropy(GpuTrainer* g, const u32* targets, i32 write_grad) {
+    cross_entropy_ex(g, targets, write_grad, 0);
 }
 
 /* Gradients of every parameter from dlogits left in g->logits
@@ -581,13 +612,15 @@ f32 gpu_trainer_forward_backward(GpuTrainer* g, const u32* ids, const u32* targe
     return mean_loss(g);
 }
 
-/* The loss rows come from the CE's statistics pass alone, so eval skips the
- * gradient pass (the reference's kernel also overwrites the logits with
- * their gradient here, which no caller can observe): same loss, bit for bit. */
+/* The loss rows come from the LM head's row statistics and target logits
+ * alone, so eval writes no logits and forms no gradient (the reference's
+ * kernel overwrites the logits with their gradient here, which no caller can
+ * observe): the same loss as forward_backward, bit for bit. */
 f32 gpu_trainer_eval_loss(GpuTrainer* g, const u32* ids, const u32* targets) {
     bind(g);
-    forward_to_logits(g, ids);
-    cross_entropy(g, targets, 0);
+    upload_targets(g, targets);
+    forward_to_loss_stats(g, ids);
+    cross_entropy_ex(g, NULL, 0, 1);
     return mean_loss(g);
 }
 
@@ -671,8 +704,8 @@ void trlm_loss_mean_queued(GpuTrainer* g, hipDeviceptr_t out, i32 acc) {
 /* eval_loss with the batch already on the device; the loss is added onto
  * *sum (acc = 0 starts the sum). */
 void trlm_eval_queued(GpuTrainer* g, hipDeviceptr_t sum, i32 acc) {
-    forward_to_logits(g, NULL);
-    cross_entropy(g, NULL, 0);
+    forward_to_loss_stats(g, NULL);
+    cross_entropy_ex(g, NULL, 0, 1);
     trlm_loss_mean_queued(g, sum, acc);
 }
 

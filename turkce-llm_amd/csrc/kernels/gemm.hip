@@ -54,6 +54,9 @@ struct GemmParams {
     const float* rope_cos;   // optional: RoPE on columns [0, rope_cols) (see rope4)
     const float* rope_sin;
     int rope_T, rope_hd, rope_cols;
+    const unsigned* tgt;     // optional, with stats: row m's target column; its value goes
+    float* tgt_val;          // to tgt_val[m] (the cross-entropy's z[t])
+    int no_store;            // with stats: C is not written (the statistics are the output)
 };
 
 // RoPE of four consecutive output columns n..n+3 of row `row` (model/rope.c:
@@ -407,7 +410,24 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                 st[0] = mx;
                 st[1] = sm;
             }
+            if (p.tgt && row < p.M) {
+                // the lane holding column t of this row (if the wave's columns
+                // include it) leaves that logit, the value C would hold
+                const int t = (int)p.tgt[row] - c0;
+                if (t >= 0 && t < BN / 2 && ((t >> 2) & 1) == half) {
+                    float v = 0.f;
+#pragma unroll
+                    for (int j = 0; j < FN; j++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++)
+#pragma unroll
+                            for (int q = 0; q < 4; q++)
+                                if (t == j * 32 + 8 * g + 4 * half + q) v = p.alpha * acc[i][j][4 * g + q];
+                    p.tgt_val[row] = v;
+                }
+            }
         }
+        if (p.no_store) return;
     }
     const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
     const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;

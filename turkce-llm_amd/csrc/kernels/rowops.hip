@@ -315,7 +315,7 @@ __device__ __forceinline__ void ms_combine(float& m, float& s, float m2, float s
 extern "C" __global__ void __launch_bounds__(256)
 k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__ targets,
                 float* __restrict__ loss_rows, int V, float grad_scale, int write_grad,
-                const float* __restrict__ stats, int nst) {
+                const float* __restrict__ stats, int nst, const float* __restrict__ zt_rows) {
     __shared__ float sm[4], ss[4];
     const long long row = blockIdx.x;
     float* z = logits + row * ld;
@@ -362,8 +362,10 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     __syncthreads();
     float M = sm[0], S = ss[0];
     for (int w = 1; w < 4; w++) ms_combine(M, S, sm[w], ss[w]);
+    // zt_rows (with stats, no gradient): the LM-head GEMM left each row's
+    // target logit and never wrote the logits
     unsigned t = targets[row];
-    float zt = z[t];
+    float zt = zt_rows ? zt_rows[row] : z[t];
     __syncthreads();
     if (threadIdx.x == 0) loss_rows[row] = (float)log((double)S) + M - zt;
     if (!write_grad) return;

@@ -42,6 +42,9 @@ typedef struct GemmParams {
     const float* rope_cos;
     const float* rope_sin;
     int rope_T, rope_hd, rope_cols;
+    const u32* tgt;
+    float* tgt_val;
+    int no_store;
 } GemmParams;
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
@@ -270,6 +273,10 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
         fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single GEMM with no beta, bias or residual\n");
         _exit(1);
     }
+    if (x && (x->tgt || x->tgt_val || x->no_store) && (!stats || (x->tgt == NULL) != (x->tgt_val == NULL))) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: target values and no_store need row statistics (and both target buffers)\n");
+        _exit(1);
+    }
     if (csum && (batch != 1 || trans_b)) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: column sums need a single GEMM with B stored [K,N]\n");
         _exit(1);
@@ -288,6 +295,11 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
     p.splits = 1; p.kchunk = K > 0 ? K : 1;
     p.alpha = alpha; p.beta = beta;
     p.csum = (float*)csum;
+    if (stats) {
+        p.tgt = (const u32*)x->tgt;
+        p.tgt_val = (float*)x->tgt_val;
+        p.no_store = x->no_store != 0;
+    }
     if (rope) {
         p.rope_cos = x->rope_cos; p.rope_sin = x->rope_sin;
         p.rope_T = x->rope_T; p.rope_hd = x->rope_hd; p.rope_cols = x->rope_cols;
