@@ -42,7 +42,9 @@ extern "C" {
 #endif
 
 /* cuda_init / cuda_init_on_device (cuda_backend.h:19,29). image_path names a
- * gfx950 code object; it is read into `scratch`. */
+ * gfx950 code object.  The context reads it into memory of its own and keeps
+ * it until hip_shutdown (the loader may refer to it while the module is
+ * loaded); `scratch`, where the reference reads its PTX, is not used. */
 HipCtx hip_init(Allocator* scratch, const char* image_path);
 HipCtx hip_init_on_device(Allocator* scratch, const char* image_path, i32 device_index);
 i32 hip_device_count(void);                                   /* cuda_backend.h:32 */

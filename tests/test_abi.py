@@ -127,6 +127,53 @@ def test_code_object_has_every_kernel(trlm):
         assert n.encode() + b"\0" in blob, n
 
 
+LLVM = "/opt/rocm/llvm/bin"
+
+
+@pytest.mark.skipif(not os.path.exists(os.path.join(LLVM, "llvm-readobj")), reason="ROCm LLVM tools not present")
+def test_kernel_argument_blocks_match_host_structs(trlm, tmp_path):
+    """Every kernel that takes an argument block by value declares, in the
+    code object's own metadata, exactly one explicit argument whose size is
+    sizeof() of the host struct the library fills (kernel_params.h, compiled
+    by the host compiler): the bytes HIP copies from the host pointer are
+    exactly the host struct, no more and no less."""
+    import yaml
+    csrc = os.path.join(ROOT, "turkce-llm_amd", "csrc")
+    src = tmp_path / "kp.c"
+    src.write_text('#include <stdio.h>\n#include "kernel_params.h"\n'
+                   'int main(void) { printf("%zu %zu %zu\\n", sizeof(GemmParams), sizeof(AttnParams), '
+                   'sizeof(DecGemmParams)); return 0; }\n')
+    exe = tmp_path / "kp"
+    subprocess.run(["gcc", "-std=c11", "-I" + csrc, str(src), "-o", str(exe)], check=True)
+    gemm, attn, dec = map(int, subprocess.run([str(exe)], check=True, capture_output=True, text=True).stdout.split())
+    co = tmp_path / "k.co"
+    subprocess.run([os.path.join(LLVM, "clang-offload-bundler"), "--unbundle", "--type=o", "--input=" + trlm.KERNELS,
+                    "--targets=hipv4-amdgcn-amd-amdhsa--gfx950", "--output=" + str(co)], check=True)
+    notes = subprocess.run([os.path.join(LLVM, "llvm-readobj"), "--notes", str(co)], check=True, capture_output=True,
+                           text=True).stdout
+    a = notes.index("---")
+    kernels = yaml.safe_load(notes[a:notes.index("\n...", a)])["amdhsa.kernels"]
+    want = {}
+    for k in kernels:
+        n = k[".name"]
+        if n.startswith("k_gemm_") and not n.startswith("k_gemm_splitk"):
+            want[n] = gemm
+        elif re.match(r"k_attn_(fwd|bwd_dkv|bwd_dq|dvec)_hd\d+$", n):
+            want[n] = attn
+        elif n in ("k_dec_qkv", "k_dec_out", "k_dec_gu", "k_dec_down", "k_dec_head"):
+            want[n] = dec
+    assert len([n for n in want if n.startswith("k_gemm_")]) == 28
+    assert len([n for n in want if n.startswith("k_attn_")]) == 12
+    assert len([n for n in want if n.startswith("k_dec_")]) == 5
+    for k in kernels:
+        n = k[".name"]
+        if n not in want:
+            continue
+        explicit = [x for x in k[".args"] if not x[".value_kind"].startswith("hidden_")]
+        assert len(explicit) == 1 and explicit[0][".value_kind"] == "by_value", (n, explicit)
+        assert explicit[0][".size"] == want[n], (n, explicit[0][".size"], want[n])
+
+
 def test_structure_layout(trlm):
     ok, got, want = trlm.check_layout()
     assert ok, (got, want)

@@ -37,34 +37,7 @@
 #define DEC_HEAD_WAVES 8u  /* waves per LM-head workgroup (as in decode_fused.hip) */
 #define DEC_HEAD_KMAX 512u /* d_model bound of the LM-head kernel's LDS rows */
 
-/* Argument block of the fused decode GEMMs; layout identical to struct
- * DecGemmParams in decode_fused.hip. */
-typedef struct DecGemmParams {
-    const float* A;
-    const u32* ids;
-    const float* E;
-    i32 a_ids, lda;
-    const float* W;
-    i32 ldw;
-    const float* bias;
-    const float* norm_w;
-    f32 eps;
-    const float* resid;
-    i32 resid_ids, ldr;
-    float* C;
-    i32 ldc;
-    i32 M, N, K;
-    i32 ncb;
-    i32 F;
-    const float* cos_t;
-    const float* sin_t;
-    const i32* pos;
-    i32 H, hd, D;
-    float* kc;
-    float* vc;
-    i32 ctx;
-    i32* pos_inc;
-} DecGemmParams;
+#include "kernel_params.h"   /* DecGemmParams: the argument block the kernels read */
 
 struct TrlmDecoder {
     GpuTrainer* g;

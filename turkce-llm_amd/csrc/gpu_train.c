@@ -121,21 +121,7 @@ static void colsum_partials(GpuTrainer* g, hipDeviceptr_t part, hipDeviceptr_t d
     hip_launch(g->k.colsum_final, cdiv_u64((u64)cols, 64), 1, 1, 256, 1, 1, 0, a2);
 }
 
-/* Attention parameter block; layout identical to struct AttnParams in attention.hip. */
-typedef struct AttnParams {
-    const float* qkv;
-    float* out;
-    const float* O;
-    const float* dO;
-    float* lse;
-    float* dvec;
-    int B, T, H, D;
-    int ldq, ldo;
-    float scale;
-    const float* rope_cos;
-    const float* rope_sin;
-    float* ds;
-} AttnParams;
+#include "kernel_params.h"   /* AttnParams: the argument block the kernels read */
 
 static AttnParams attn_params(GpuTrainer* g) {
     AttnParams a;

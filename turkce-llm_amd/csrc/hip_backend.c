@@ -16,6 +16,7 @@ struct HipAllocList {
     void** ptrs;
     u64 count;
     u64 cap;
+    void* image;   /* the loaded code object's bytes, owned until hip_shutdown */
 };
 
 struct HipSide {
@@ -42,7 +43,12 @@ static void check(hipError_t r, const char* what) {
     }
 }
 
-static void* read_image(Allocator* scratch, const char* path, u64* out_size) {
+/* The code object is read into memory the context owns and keeps until
+ * hip_shutdown has unloaded the module: the HSA loader may keep referring to
+ * the bytes a code object was loaded from (a reader created from memory
+ * must outlive the loaded object), so they must not live in an arena the
+ * caller may reset or free while the module is loaded. */
+static void* read_image(const char* path, u64* out_size) {
     FILE* f = fopen(path, "rb");
     if (!f) {
         fprintf(stderr, "[HIP ERROR] cannot open kernel image: %s\n", path);
@@ -51,7 +57,11 @@ static void* read_image(Allocator* scratch, const char* path, u64* out_size) {
     fseek(f, 0, SEEK_END);
     long size = ftell(f);
     fseek(f, 0, SEEK_SET);
-    u8* buf = scratch ? (u8*)allocator_alloc(scratch, (u64)size + 1) : (u8*)malloc((size_t)size + 1);
+    u8* buf = (u8*)malloc((size_t)size + 1);
+    if (!buf) {
+        fprintf(stderr, "[HIP ERROR] out of host memory for kernel image: %s\n", path);
+        fatal_exit();
+    }
     size_t got = fread(buf, 1, (size_t)size, f);
     fclose(f);
     if (got != (size_t)size) {
@@ -78,13 +88,14 @@ HipCtx hip_init_on_device(Allocator* scratch, const char* image_path, i32 device
     }
     c.device = device_index;
     check(hipSetDevice(device_index), "hipSetDevice");
+    (void)scratch;   /* the reference reads the image into it; here the context owns the bytes */
     u64 size;
-    void* image = read_image(scratch, image_path, &size);
+    void* image = read_image(image_path, &size);
     check(hipModuleLoadData(&c.module, image), "hipModuleLoadData");
-    if (!scratch) free(image);
     check(hipStreamCreateWithFlags(&c.stream, hipStreamNonBlocking), "hipStreamCreateWithFlags");
     c.allocs = (HipAllocList*)calloc(1, sizeof(HipAllocList));
     pthread_mutex_init(&c.allocs->lock, NULL);
+    c.allocs->image = image;
     return c;
 }
 
@@ -105,6 +116,7 @@ void hip_shutdown(HipCtx* c) {
     if (c->side) check(hipStreamSynchronize(c->side->stream), "hipStreamSynchronize");
     for (u64 i = 0; i < c->allocs->count; i++)
         if (c->allocs->ptrs[i]) check(hipFree(c->allocs->ptrs[i]), "hipFree");
+    void* image = c->allocs->image;
     free(c->allocs->ptrs);
     pthread_mutex_destroy(&c->allocs->lock);
     free(c->allocs);
@@ -120,6 +132,7 @@ void hip_shutdown(HipCtx* c) {
     }
     check(hipStreamDestroy(c->stream), "hipStreamDestroy");
     check(hipModuleUnload(c->module), "hipModuleUnload");
+    free(image);
     if (tls_ctx == c) tls_ctx = NULL;
 }
 

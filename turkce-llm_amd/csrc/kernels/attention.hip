@@ -36,28 +36,7 @@
 
 #define ATT_LOG2E 1.4426950408889634f
 
-struct AttnParams {
-    const float* qkv;  // [B*T, ldq]
-    float* out;        // forward: O [B*T, ldo]; backward: dqkv [B*T, ldq]
-    const float* O;    // backward: O [B*T, ldo]
-    const float* dO;   // backward: dO [B*T, ldo]
-    float* lse;        // [B*H*T] base-2 log-sum-exp of scaled scores
-    float* dvec;       // [B*H*T] D_i = <dO_i, O_i>
-    int B, T, H, D;
-    int ldq, ldo;
-    float scale;       // 1/sqrt(HD)
-    // backward: when set, dQ and dK leave through the transpose of the RoPE
-    // rotation (tables [T][HD/2]), so dqkv is the gradient of the un-rotated
-    // projection
-    const float* rope_cos;
-    const float* rope_sin;
-    // backward: the dK/dV pass leaves every causal 64x64 block of
-    // dS = P o (dP - D) * scale here for the dQ pass: [B*H][nqb(nqb+1)/2]
-    // blocks (query block i, key block j <= i at i(i+1)/2 + j), each in the
-    // dK/dV pass's register order [key group g][query half c][r][lane]: key
-    // 32g + l%32, query 32c + 8(r/4) + 4(l/32) + r%4 (one 256-byte row per r)
-    float* ds;
-};
+#include "../kernel_params.h"   // GemmParams, AttnParams, DecGemmParams
 
 // First float of dS block (query block qb, key block kb <= qb) of head bh.
 __device__ __forceinline__ float* att_ds_block(const AttnParams& p, int bh, int qb, int kb) {

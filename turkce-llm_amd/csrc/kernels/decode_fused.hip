@@ -39,34 +39,7 @@ enum { DM_PLAIN = 0, DM_QKV = 1, DM_SWIGLU = 2 };
 
 // Argument block of the fused GEMMs; layout mirrored by DecGemmParams in
 // gpu_decode.c.
-struct DecGemmParams {
-    const float* A;          // [M, lda] (unused when a_ids)
-    const unsigned* ids;     // token ids [M] for a_ids / resid_ids
-    const float* E;          // embedding table [V, D] for ids
-    int a_ids;               // row m of A is E[ids[m]] (layer 0's input), row stride lda
-    int lda;
-    const float* W;          // NN: [K, ldw]; NT: [N, ldw] (the head's E)
-    int ldw;
-    const float* bias;       // [N] or null
-    const float* norm_w;     // RMSNorm weight [K] (kernels with the norm prologue)
-    float eps;
-    const float* resid;      // [M, ldr] or null
-    int resid_ids;           // row m of resid is E[ids[m]] (layer 0), row stride ldr
-    int ldr;
-    float* C;                // [M, ldc]
-    int ldc;
-    int M, N, K;
-    int ncb;                 // column blocks of 16
-    int F;                   // SwiGLU: the up half starts at column F; h has F columns
-    const float* cos_t;      // QKV: RoPE tables [ctx][hd/2]
-    const float* sin_t;
-    const int* pos;          // the token's position (device-resident)
-    int H, hd, D;
-    float* kc;               // this layer's caches [M][H][ctx][hd]
-    float* vc;
-    int ctx;
-    int* pos_inc;            // head: block 0 adds 1 to *pos_inc after its stores
-};
+#include "../kernel_params.h"   // GemmParams, AttnParams, DecGemmParams
 
 __device__ __forceinline__ f32x4_t ld4(const float* p) { return *(const f32x4_t*)p; }
 

@@ -35,29 +35,7 @@
 
 #include <type_traits>
 
-struct GemmParams {
-    const float* A;
-    const float* B;
-    float* C;
-    const float* bias;
-    const float* resid;
-    long long sA, sB, sC, sW;
-    int M, N, K;
-    int lda, ldb, ldc, ldr;
-    int splits, kchunk;
-    float alpha, beta;
-    int tiles_m, tiles_n;
-    float* stats;      // optional: per-row (max, sum exp(v - max)) of each wave's columns
-    int stats_ld;      // float2 entries per row of stats
-    float* csum;       // optional (TB = 0): column sums of B over k (a bias gradient);
-                       // with split-K each split writes its partial as row M of its slab
-    const float* rope_cos;   // optional: RoPE on columns [0, rope_cols) (see rope4)
-    const float* rope_sin;
-    int rope_T, rope_hd, rope_cols;
-    const unsigned* tgt;     // optional, with stats: row m's target column; its value goes
-    float* tgt_val;          // to tgt_val[m] (the cross-entropy's z[t])
-    int no_store;            // with stats: C is not written (the statistics are the output)
-};
+#include "../kernel_params.h"   // GemmParams, AttnParams, DecGemmParams
 
 // RoPE of four consecutive output columns n..n+3 of row `row` (model/rope.c:
 // 20-40): pairs (2k, 2k+1) of a head of rope_hd columns rotated by

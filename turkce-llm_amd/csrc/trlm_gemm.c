@@ -23,29 +23,7 @@
 
 #include "gpu_internal.h"
 
-/* Kernel argument block; layout identical to struct GemmParams in gemm.hip. */
-typedef struct GemmParams {
-    const float* A;
-    const float* B;
-    float* C;
-    const float* bias;
-    const float* resid;
-    long long sA, sB, sC, sW;
-    int M, N, K;
-    int lda, ldb, ldc, ldr;
-    int splits, kchunk;
-    float alpha, beta;
-    int tiles_m, tiles_n;
-    float* stats;
-    int stats_ld;
-    float* csum;
-    const float* rope_cos;
-    const float* rope_sin;
-    int rope_T, rope_hd, rope_cols;
-    const u32* tgt;
-    float* tgt_val;
-    int no_store;
-} GemmParams;
+#include "kernel_params.h"   /* GemmParams: the argument block the kernels read */
 
 enum { L_NN = 0, L_NT = 1, L_TN = 2 };
 static const char* LAYOUT_NAME[4] = { "nn", "nt", "tn", "tt" };
