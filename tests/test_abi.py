@@ -103,7 +103,7 @@ def test_undefined_symbols_are_runtime_only(trlm):
     other = {n for n in names if not (n.startswith("hip") or n.startswith("_") or n in runtime)}
     libc = {"fprintf", "fflush", "_exit", "fopen", "fseek", "ftell", "fread", "fclose", "malloc", "calloc",
             "realloc", "free", "memset", "memcpy", "memcmp", "strcmp", "strlen", "snprintf", "fwrite", "rename",
-            "remove", "stderr", "stdout", "clock_gettime", "getenv",
+            "remove", "stderr", "stdout", "clock_gettime", "getenv", "pthread_create", "pthread_join",
             "pthread_mutex_lock", "pthread_mutex_unlock", "pthread_mutex_init", "pthread_mutex_destroy"}
     assert other <= libc, other - libc
     assert runtime & names == runtime, runtime - names

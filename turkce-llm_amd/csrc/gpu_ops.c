@@ -34,6 +34,8 @@ typedef struct Slot {
     TrlmGemm* gemm;
     hipDeviceptr_t buf[3];
     u64 cap[3];
+    void* stage;        /* pinned host staging for results (grow-only) */
+    u64 stage_cap;
 } Slot;
 
 static Slot g_slots[MAX_GPU_CONTEXTS];
@@ -105,6 +107,11 @@ void gpu_ops_set_worker_id(i32 worker_id) { g_tls_worker_id = worker_id; }
 
 static void slot_release(u32 s) {
     hip_set_current(&g_slots[s].ctx);
+    if (g_slots[s].stage) {
+        hipHostFree(g_slots[s].stage);
+        g_slots[s].stage = NULL;
+        g_slots[s].stage_cap = 0;
+    }
     trlm_gemm_destroy(g_slots[s].gemm);
     g_slots[s].gemm = NULL;
     hip_shutdown(&g_slots[s].ctx);
@@ -176,6 +183,63 @@ static hipDeviceptr_t slot_buf(Slot* s, u32 which, u64 bytes) {
         s->cap[which] = bytes;
     }
     return s->buf[which];
+}
+
+/* A result goes to the caller's tensor through the slot's pinned staging
+ * buffer: the DMA runs at pinned-memory speed, and the copy into the
+ * tensor -- freshly carved arena pages, each faulted in on first touch --
+ * is split over up to D2H_THREADS host threads, which take their page
+ * faults in parallel.  Small results are copied directly. */
+#define D2H_THREADS 8
+#define D2H_MIN_PART (1ull << 20)
+typedef struct CopyPart { u8* dst; const u8* src; u64 n; } CopyPart;
+
+static void* copy_part(void* arg) {
+    CopyPart* c = (CopyPart*)arg;
+    memcpy(c->dst, c->src, c->n);
+    return NULL;
+}
+
+static void d2h_result(Slot* s, f32* dst, hipDeviceptr_t src, u64 bytes) {
+    if (bytes < 2 * D2H_MIN_PART) {
+        hip_d2h(dst, src, bytes);
+        return;
+    }
+    if (s->stage_cap < bytes) {
+        if (s->stage) hipHostFree(s->stage);
+        s->stage = NULL;
+        hipError_t r = hipHostMalloc(&s->stage, bytes, hipHostMallocDefault);
+        if (r != hipSuccess) {
+            fprintf(stderr, "[HIP ERROR] gpu_ops: hipHostMalloc of %llu bytes -> %s\n", (unsigned long long)bytes,
+                    hipGetErrorName(r));
+            _exit(1);
+        }
+        s->stage_cap = bytes;
+    }
+    hipError_t r = hipMemcpyDtoHAsync(s->stage, src, bytes, s->ctx.stream);
+    if (r == hipSuccess) r = hipStreamSynchronize(s->ctx.stream);
+    if (r != hipSuccess) {
+        fprintf(stderr, "[HIP ERROR] gpu_ops: result download -> %s\n", hipGetErrorName(r));
+        _exit(1);
+    }
+    u64 nt = bytes / D2H_MIN_PART;
+    if (nt > D2H_THREADS) nt = D2H_THREADS;
+    const u64 per = ((bytes + nt - 1) / nt + 63) & ~63ull;
+    CopyPart parts[D2H_THREADS];
+    pthread_t th[D2H_THREADS];
+    int started[D2H_THREADS];
+    for (u64 i = 0; i < nt; i++) {
+        const u64 off = i * per < bytes ? i * per : bytes;
+        parts[i].dst = (u8*)dst + off;
+        parts[i].src = (const u8*)s->stage + off;
+        parts[i].n = (off + per < bytes ? off + per : bytes) - off;
+        started[i] = i > 0 && pthread_create(&th[i], NULL, copy_part, &parts[i]) == 0;
+    }
+    copy_part(&parts[0]);
+    for (u64 i = 1; i < nt; i++) {
+        if (started[i]) pthread_join(th[i], NULL);
+        else copy_part(&parts[i]);
+    }
 }
 
 /* How a 2-D view is laid out in host memory. */
@@ -253,7 +317,7 @@ static Tensor gpu_matmul(Allocator* alloc, const Tensor* a, const Tensor* b) {
     hipDeviceptr_t dc = slot_buf(s, 2, (M * N > 0 ? M * N : 1) * sizeof(f32));
     trlm_gemm(s->gemm, va.trans, vb.trans, da, db, dc, (i32)M, (i32)N, (i32)K, (i32)lda, (i32)ldb,
               (i32)N, 1, 0, 0, 0, 1.0f, 0.0f, NULL, NULL, (i32)N);
-    hip_d2h(out.data, dc, M * N * sizeof(f32));
+    d2h_result(s, out.data, dc, M * N * sizeof(f32));
 
     if (!own) pthread_mutex_unlock(&g_slot0_mutex);
     pthread_mutex_lock(&g_debug_mutex);
