@@ -69,12 +69,23 @@ static u32 swiglu_blocks(const GpuTrainer* g, u64 rows) {
     return cdiv_u64(work, 256);
 }
 
+/* float4 chunks per lane of the 16-lanes-per-row RMSNorm kernels for
+ * rows of D floats (k_rmsnorm_{fwd,bwd}_q<n>), 0 when D needs the generic
+ * one-wave-per-row kernels (D % 4 != 0 or D > 1024). */
+static u32 rms_nq(u32 D) {
+    static const u32 NQ[] = { 1, 2, 4, 6, 8, 16 };
+    if (D % 4 || D > 1024) return 0;
+    for (u32 i = 0; i < sizeof(NQ) / sizeof(NQ[0]); i++)
+        if (64 * NQ[i] >= D) return NQ[i];
+    return 0;
+}
+
 static void rmsnorm_rows(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv,
                          u32 nrows) {
     i32 rows = (i32)nrows, cols = (i32)g->D;
     f32 eps = g->eps;
     void* args[] = { &x, &w, &out, &rinv, &rows, &cols, &eps };
-    hip_launch(g->k.rmsnorm_fwd, cdiv_u64(nrows, 4), 1, 1, 256, 1, 1, 0, args);
+    hip_launch(g->k.rmsnorm_fwd, cdiv_u64(nrows, rms_nq(g->D) ? 16 : 4), 1, 1, 256, 1, 1, 0, args);
 }
 
 static void rmsnorm_fwd(GpuTrainer* g, hipDeviceptr_t x, hipDeviceptr_t w, hipDeviceptr_t out, hipDeviceptr_t rinv) {
@@ -233,8 +244,19 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     HipCtx* c = &g.hip;
     g.k.embed_fwd = hip_get_kernel(c, "k_embed_fwd");
     g.k.embed_bwd = hip_get_kernel(c, "k_embed_bwd");
-    g.k.rmsnorm_fwd = hip_get_kernel(c, "k_rmsnorm_fwd");
-    g.k.rmsnorm_bwd = hip_get_kernel(c, "k_rmsnorm_bwd");
+    {
+        const u32 nq = rms_nq(g.D);
+        char fname[40], bname[40];
+        if (nq) {
+            snprintf(fname, sizeof(fname), "k_rmsnorm_fwd_q%u", nq);
+            snprintf(bname, sizeof(bname), "k_rmsnorm_bwd_q%u", nq);
+        } else {
+            snprintf(fname, sizeof(fname), "k_rmsnorm_fwd");
+            snprintf(bname, sizeof(bname), "k_rmsnorm_bwd");
+        }
+        g.k.rmsnorm_fwd = hip_get_kernel(c, fname);
+        g.k.rmsnorm_bwd = hip_get_kernel(c, bname);
+    }
     g.k.colsum_final = hip_get_kernel(c, "k_colsum_final");
     g.k.swiglu_fwd = hip_get_kernel(c, "k_swiglu_fwd");
     g.k.swiglu_bwd = hip_get_kernel(c, "k_swiglu_bwd");

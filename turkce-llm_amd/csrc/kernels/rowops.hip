@@ -192,6 +192,131 @@ k_rmsnorm_bwd(const float* __restrict__ x, const float* __restrict__ w, const fl
     }
 }
 
+// ---------------------------------------------------------------- RMSNorm, 16 lanes per row
+// The same two kernels for rows of cols % 4 == 0, cols <= 64 * NQ floats:
+// 16 lanes per row, 4 rows per wave, 16 rows per 256-thread block, lane s
+// of a row holding its float4 chunks s, s + 16, ... (NQ of them, chosen per
+// model so that no load is wasted).  Every load of a row is issued before
+// any arithmetic, from a clamped (valid) address, and masked afterwards:
+// one memory latency per row instead of one per dependent step.  The
+// row's reductions are 16-lane butterflies.
+__device__ __forceinline__ float rms_sum16(float v) {
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) v += __shfl_xor(v, m, WAVE);
+    return v;
+}
+
+template <int NQ>
+__device__ __forceinline__ void rmsnorm_fwd_q(const float* __restrict__ x, const float* __restrict__ w,
+                                              float* __restrict__ out, float* __restrict__ rinv, int rows,
+                                              int cols, float eps) {
+    const int lane = threadIdx.x & 63, sl = lane & 15;
+    int row = blockIdx.x * 16 + (threadIdx.x >> 6) * 4 + (lane >> 4);
+    const bool rv = row < rows;
+    if (!rv) row = rows - 1;
+    const int c4 = cols >> 2;
+    const float* xr = x + (long long)row * cols;
+    f32x4 v[NQ], wv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int q = sl + 16 * i, qc = q < c4 ? q : 0;
+        v[i] = *(const f32x4*)(xr + 4 * qc);
+        wv[i] = *(const f32x4*)(w + 4 * qc);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; i++)
+        if (sl + 16 * i < c4) ss += v[i][0] * v[i][0] + v[i][1] * v[i][1] + v[i][2] * v[i][2] + v[i][3] * v[i][3];
+    ss = rms_sum16(ss);
+    const float r = 1.0f / (float)sqrt((double)(ss / (float)cols + eps));
+    if (rv && sl == 0) rinv[row] = r;
+    float* orow = out + (long long)row * cols;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int q = sl + 16 * i;
+        if (rv && q < c4) {
+            f32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; e++) o[e] = v[i][e] * r * wv[i][e];
+            *(f32x4*)(orow + 4 * q) = o;
+        }
+    }
+}
+
+// Backward as k_rmsnorm_bwd; the weight-gradient partial of a wave's four
+// rows is added across them by butterfly (rows (0+1)+(2+3)), and the four
+// waves' partials in wave order, into the block's partial row.
+template <int NQ>
+__device__ __forceinline__ void rmsnorm_bwd_q(const float* __restrict__ x, const float* __restrict__ w,
+                                              const float* __restrict__ rinv, const float* __restrict__ dy,
+                                              const float* __restrict__ dxin, float* __restrict__ dx,
+                                              float* __restrict__ wpart, int rows, int cols) {
+    extern __shared__ float part[];   // [4][cols]
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, sl = lane & 15;
+    int row = blockIdx.x * 16 + wave * 4 + (lane >> 4);
+    const bool rv = row < rows;
+    if (!rv) row = rows - 1;
+    const int c4 = cols >> 2;
+    const long long ro = (long long)row * cols;
+    f32x4 wv[NQ], xv[NQ], dv[NQ], gv[NQ];
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int q = sl + 16 * i, qc = q < c4 ? q : 0;
+        wv[i] = *(const f32x4*)(w + 4 * qc);
+        xv[i] = *(const f32x4*)(x + ro + 4 * qc);
+        dv[i] = *(const f32x4*)(dy + ro + 4 * qc);
+        gv[i] = dxin ? *(const f32x4*)(dxin + ro + 4 * qc) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    const float r = rinv[row];
+    float S = 0.f;
+#pragma unroll
+    for (int i = 0; i < NQ; i++)
+        if (sl + 16 * i < c4)
+#pragma unroll
+            for (int e = 0; e < 4; e++) S += dv[i][e] * wv[i][e] * xv[i][e];
+    S = rms_sum16(S);
+    const float c = r * r * r / (float)cols;
+    float* g = dx + ro;
+#pragma unroll
+    for (int i = 0; i < NQ; i++) {
+        const int q = sl + 16 * i;
+        const bool ok = q < c4;
+        f32x4 o, a;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            o[e] = gv[i][e] + (wv[i][e] * r * dv[i][e] - c * xv[i][e] * S);
+            a[e] = (rv && ok) ? dv[i][e] * xv[i][e] * r : 0.f;
+        }
+        if (rv && ok) *(f32x4*)(g + 4 * q) = o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            a[e] += __shfl_xor(a[e], 16, WAVE);
+            a[e] += __shfl_xor(a[e], 32, WAVE);
+        }
+        if (lane < 16 && ok) *(f32x4*)(part + wave * cols + 4 * q) = a;
+    }
+    __syncthreads();
+    for (int j = threadIdx.x; j < cols; j += 256)
+        wpart[(long long)blockIdx.x * cols + j] = ((part[j] + part[cols + j]) + part[2 * cols + j]) + part[3 * cols + j];
+}
+
+#define RMS_Q_KERNELS(NQ)                                                                                      \
+    extern "C" __global__ void __launch_bounds__(256)                                                          \
+    k_rmsnorm_fwd_q##NQ(const float* x, const float* w, float* out, float* rinv, int rows, int cols, float eps) { \
+        rmsnorm_fwd_q<NQ>(x, w, out, rinv, rows, cols, eps);                                                 \
+    }                                                                                                          \
+    extern "C" __global__ void __launch_bounds__(256)                                                          \
+    k_rmsnorm_bwd_q##NQ(const float* x, const float* w, const float* rinv, const float* dy, const float* dxin, \
+                        float* dx, float* wpart, int rows, int cols) {                                          \
+        rmsnorm_bwd_q<NQ>(x, w, rinv, dy, dxin, dx, wpart, rows, cols);                                      \
+    }
+RMS_Q_KERNELS(1)
+RMS_Q_KERNELS(2)
+RMS_Q_KERNELS(4)
+RMS_Q_KERNELS(6)
+RMS_Q_KERNELS(8)
+RMS_Q_KERNELS(16)
+
 // ---------------------------------------------------------------- column sums
 // out[c] (+)= sum over b of partial[b, c] (the RMSNorm weight gradient's
 // per-block partials), over the partial rows of row group blockIdx.y
