@@ -49,7 +49,11 @@ void trlm_argmax_rows(GpuTrainer* g, hipDeviceptr_t logits, i32 ld, u32 rows, hi
  *   tgt / tgt_val (with stats): tgt_val[m] = C[m, tgt[m]], the value the
  *          epilogue computes for that element (tgt[m] < N);
  *   no_store (with stats): C is not written -- the statistics (and tgt_val)
- *          are the whole output.
+ *          are the whole output;
+ *   glu_h / glu_F: the gate/up projection with its SwiGLU: C = [gate | up]
+ *          (N = 2 glu_F) is written as usual and glu_h [M, glu_F] receives
+ *          silu(gate) * up; single aligned NN GEMM, glu_F % 32 == 0,
+ *          K % 32 == 0, bias allowed, nothing else.
  * Returns the stats entries written per row (0 without stats). */
 typedef struct TrlmGemmExtra {
     hipDeviceptr_t stats;
@@ -61,6 +65,8 @@ typedef struct TrlmGemmExtra {
     hipDeviceptr_t tgt;
     hipDeviceptr_t tgt_val;
     i32 no_store;
+    hipDeviceptr_t glu_h;
+    i32 glu_F;
 } TrlmGemmExtra;
 i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,

@@ -441,9 +441,18 @@ void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void
         gemm1(g, GEMM_NN, a->att, P_(g, pidx(l, PK_WO)), a->x2, N, D, D, D, D, D, 0.0f, P_(g, pidx(l, PK_BO)),
               a->x_in);
         rmsnorm_fwd(g, a->x2, P_(g, pidx(l, PK_FFN_NORM)), a->n2, a->r2);
-        gemm1(g, GEMM_NN, a->n2, P_(g, pidx(l, PK_WGU)), a->gu, N, 2 * F, D, D, 2 * F, 2 * F, 0.0f,
-              P_(g, pidx(l, PK_BGU)), NULL);
-        {
+        /* gu = n2 @ Wgu + bgu, and h = SwiGLU(gu): in the GEMM's epilogue
+         * where the widths allow it, else as a separate pass */
+        if (F % 32 == 0 && D % 32 == 0) {
+            TrlmGemmExtra x;
+            memset(&x, 0, sizeof(x));
+            x.glu_h = a->h;
+            x.glu_F = F;
+            trlm_gemm_ex(g->gemm, 0, 0, a->n2, P_(g, pidx(l, PK_WGU)), a->gu, N, 2 * F, D, D, 2 * F, 2 * F, 1, 0, 0,
+                         0, 1.0f, 0.0f, P_(g, pidx(l, PK_BGU)), NULL, 2 * F, &x);
+        } else {
+            gemm1(g, GEMM_NN, a->n2, P_(g, pidx(l, PK_WGU)), a->gu, N, 2 * F, D, D, 2 * F, 2 * F, 0.0f,
+                  P_(g, pidx(l, PK_BGU)), NULL);
             hipDeviceptr_t gu = a->gu, h = a->h;
             void* args[] = { &gu, &h, &N, &F };
             hip_launch(g->k.swiglu_fwd, swiglu_blocks(g, (u64)N), 1, 1, 256, 1, 1, 0, args);

@@ -29,6 +29,8 @@ typedef struct GemmParams {
     const unsigned* tgt;     // optional, with stats: row m's target column; its value goes
     float* tgt_val;          // to tgt_val[m] (the cross-entropy's z[t])
     int no_store;            // with stats: C is not written (the statistics are the output)
+    float* glu_h;            // optional (SwiGLU epilogue, k_gemm_nn_64x64_k32_glu): h [M, glu_F] =
+    int glu_F;               // silu(gate) * up of C = [gate | up] (N = 2 * glu_F), C still written
 } GemmParams;
 
 /* Flash attention (kernels/attention.hip, host gpu_train.c) */

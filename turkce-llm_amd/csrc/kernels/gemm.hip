@@ -162,7 +162,10 @@ struct TileStream {
     static constexpr int NL = R * BK / 4 / 256;
     const float* ptr[NL];
     long long step;
-    __device__ __forceinline__ void init(const float* __restrict__ base, int ld, int r0, int rlim, int k0) {
+    // glu_F (m/n-major, R = 64): the tile's columns 0..31 are gate columns
+    // r0/2 .. of [gate | up] and 32..63 the matching up columns glu_F + r0/2 ..
+    __device__ __forceinline__ void init(const float* __restrict__ base, int ld, int r0, int rlim, int k0,
+                                         int glu_F = 0) {
         const int t = threadIdx.x;
 #pragma unroll
         for (int i = 0; i < NL; i++) {
@@ -171,6 +174,7 @@ struct TileStream {
             if (KMAJOR) { r = idx / (BK / 4); k = (idx % (BK / 4)) * 4; }
             else { k = idx / (R / 4); r = (idx % (R / 4)) * 4; }
             int gr = r0 + r;
+            if (!KMAJOR && glu_F) gr = (r < 32 ? 0 : glu_F - 32) + (r0 >> 1) + r;
             if (gr >= rlim) gr = KMAJOR ? rlim - 1 : 0;
             ptr[i] = KMAJOR ? base + (long long)gr * ld + (k0 + k) : base + (long long)(k0 + k) * ld + gr;
         }
@@ -490,12 +494,60 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
     }
 }
 
+// SwiGLU epilogue of the gate/up projection (64x64 tiles, the B columns of
+// tile tn paired as gate r0/2 + 0..31 and up glu_F + r0/2 + 0..31, see
+// TileStream): every wave stores its 32x32 block of C = [gate | up] (+ bias)
+// at the real columns, the up waves hand their values to the gate waves
+// through LDS, and those store h = (g * sigmoid(g)) * u (feedforward.c:
+// 146-150, the order of k_swiglu_fwd) -- the separate SwiGLU pass and its
+// re-read of C disappear.
+__device__ __forceinline__ void gemm_epilogue_glu(const GemmParams& p, const f32x16& acc, int r0, int tn, int wm,
+                                                  int wn, int lane, float* lds) {
+    const int half = lane >> 5, ml = lane & 31;
+    const int row = r0 + ml;
+    const int cb = (wn == 0 ? 0 : p.glu_F) + 32 * tn;
+    f32x4 v[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+        const int n = cb + 8 * g + 4 * half;
+        const f32x4 b = p.bias ? *(const f32x4*)(p.bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            float x = p.alpha * acc[4 * g + q];
+            if (p.bias) x = x + b[q];
+            v[g][q] = x;
+        }
+        if (row < p.M) *(f32x4*)(p.C + (long long)row * p.ldc + n) = v[g];
+    }
+    constexpr int LDX = 36;
+    float* xs = lds + wm * 32 * LDX;
+    __syncthreads();   // the main loop's last LDS reads are done
+    if (wn == 1) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) *(f32x4*)(xs + ml * LDX + 8 * g + 4 * half) = v[g];
+    }
+    __syncthreads();
+    if (wn == 0 && row < p.M) {
+#pragma unroll
+        for (int g = 0; g < 4; g++) {
+            const f32x4 u = *(const f32x4*)(xs + ml * LDX + 8 * g + 4 * half);
+            f32x4 o;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float sg = 1.0f / (1.0f + expf(-v[g][q]));
+                o[q] = (v[g][q] * sg) * u[q];
+            }
+            *(f32x4*)(p.glu_h + (long long)row * p.glu_F + 32 * tn + 8 * g + 4 * half) = o;
+        }
+    }
+}
+
 // As gemm_mainloop_full, with the global loads two tiles ahead: tile j >= 1
 // is staged in register set (j - 1) & 1, so the load of tile kt + 3 is
 // issued at the end of tile kt and has two tiles of MFMAs to land before
 // its LDS store at the end of tile kt + 2.  The k loop is unrolled by two so
 // that the register set and the LDS buffer are compile-time indices.
-template <int TA, int TB, int BM, int BN, int BK>
+template <int TA, int TB, int BM, int BN, int BK, bool GLU = false>
 __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const float* A, const float* B, int m0,
                                                   int n0, int kb, int ke, float* lds,
                                                   f32x16 (&acc)[BM / 64][BN / 64], bool cs_on, f32x4& cs) {
@@ -514,7 +566,7 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
     TileStream<BM, BK, AK> sa;
     TileStream<BN, BK, BK_> sb;
     sa.init(A, p.lda, m0, p.M, kb);
-    sb.init(B, p.ldb, n0, p.N, kb);
+    sb.init(B, p.ldb, n0, p.N, kb, GLU ? p.glu_F : 0);
     const int nk = (ke - kb) / BK;
     sa.load(ra[0]);
     sb.load(rb[0]);
@@ -589,7 +641,7 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
     }
 }
 
-template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED, int PF = 1>
+template <int TA, int TB, int BM, int BN, int BK, bool ALIGNED, int PF = 1, bool GLU = false>
 __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     constexpr bool AK = (TA == 0);   // A K-contiguous
     constexpr bool BK_ = (TB == 1);  // B K-contiguous
@@ -631,7 +683,7 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     f32x4 cs = {0.f, 0.f, 0.f, 0.f};
     if constexpr (ALIGNED) {
         if (kfull > kb) {
-            if constexpr (PF == 2) gemm_mainloop_pf2<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, kfull, lds, acc, cs_on, cs);
+            if constexpr (PF == 2) gemm_mainloop_pf2<TA, TB, BM, BN, BK, GLU>(p, A, B, m0, n0, kb, kfull, lds, acc, cs_on, cs);
             else gemm_mainloop_full<TA, TB, BM, BN, BK>(p, A, B, m0, n0, kb, kfull, lds, acc, cs_on, cs);
         }
         if (kfull < ke) {
@@ -659,7 +711,12 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
         }
     }
 
-    gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
+    if constexpr (GLU) {
+        static_assert(BM == 64 && BN == 64 && PF == 2 && ALIGNED, "SwiGLU epilogue: 64x64 pipelined tiles");
+        gemm_epilogue_glu(p, acc[0][0], m0 + wm0, tn, wave >> 1, wave & 1, lane, lds);
+    } else {
+        gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
+    }
 }
 
 #define GEMM_KERNEL(NAME, TA, TB, BM, BN, BK, AL, WPE, PF)                             \
@@ -689,6 +746,11 @@ GEMM_LAYOUTS(64x128, 64, 128, 16, 4, 1)
 GEMM_LAYOUTS(64x128_k32, 64, 128, 32, 2, 2)
 GEMM_LAYOUTS(64x64, 64, 64, 16, 5, 1)
 GEMM_LAYOUTS(64x64_k32, 64, 64, 32, 4, 2)
+// the gate/up projection with the SwiGLU epilogue (host: K % 32 == 0, N = 2F, F % 32 == 0)
+extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(4)))
+k_gemm_nn_64x64_k32_glu(GemmParams p) {
+    gemm_body<0, 0, 64, 64, 32, true, 2, true>(p);
+}
 GEMM_KERNEL(k_gemm_nn_64x64_u, 0, 0, 64, 64, 16, false, 1, 1)
 GEMM_KERNEL(k_gemm_nt_64x64_u, 0, 1, 64, 64, 16, false, 1, 1)
 GEMM_KERNEL(k_gemm_tn_64x64_u, 1, 0, 64, 64, 16, false, 1, 1)

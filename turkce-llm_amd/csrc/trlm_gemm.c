@@ -45,6 +45,7 @@ struct TrlmGemm {
     hipFunction_t k[3][T_COUNT];
     hipFunction_t ku[4];
     hipFunction_t reduce;
+    hipFunction_t glu;   /* k_gemm_nn_64x64_k32_glu */
     hipDeviceptr_t ws;
     u64 ws_floats;
     char last[48];
@@ -68,6 +69,7 @@ TrlmGemm* trlm_gemm_create(HipCtx* ctx) {
         e->ku[l] = hip_get_kernel(ctx, name);
     }
     e->reduce = hip_get_kernel(ctx, "k_gemm_splitk_reduce");
+    e->glu = hip_get_kernel(ctx, "k_gemm_nn_64x64_k32_glu");
     trlm_noalloc_setup(ctx->device);
     return e;
 }
@@ -254,6 +256,28 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
     if (x && (x->tgt || x->tgt_val || x->no_store) && (!stats || (x->tgt == NULL) != (x->tgt_val == NULL))) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: target values and no_store need row statistics (and both target buffers)\n");
         _exit(1);
+    }
+    if (x && x->glu_h) {
+        /* the SwiGLU epilogue: one fixed kernel, so only the shapes it tiles exactly */
+        if (trans_a || trans_b || batch != 1 || beta != 0.0f || resid || stats || csum || rope || fixed_ws ||
+            x->glu_F <= 0 || x->glu_F % 32 || N != 2 * x->glu_F || K <= 0 || K % 32 || !aligned16(A) ||
+            !aligned16(B) || !aligned16(C) || !aligned16(x->glu_h) || lda % 4 || ldb % 4 || ldc % 4 ||
+            (bias && !aligned16(bias))) {
+            fprintf(stderr, "[HIP ERROR] trlm_gemm: the SwiGLU epilogue needs a single aligned NN GEMM, N = 2F with "
+                            "F %% 32 == 0, K %% 32 == 0, no beta, residual or other epilogue\n");
+            _exit(1);
+        }
+        GemmParams p;
+        memset(&p, 0, sizeof(p));
+        p.A = (const float*)A; p.B = (const float*)B; p.C = (float*)C; p.bias = (const float*)bias;
+        p.M = M; p.N = N; p.K = K; p.lda = lda; p.ldb = ldb; p.ldc = ldc; p.ldr = ldr;
+        p.splits = 1; p.kchunk = K; p.alpha = alpha; p.beta = 0.0f;
+        p.tiles_m = cdiv(M, 64); p.tiles_n = cdiv(N, 64);
+        p.glu_h = (float*)x->glu_h; p.glu_F = x->glu_F;
+        snprintf(e->last, sizeof(e->last), "k_gemm_nn_64x64_k32_glu");
+        e->last_splits = 1;
+        launch(e->glu, &p, 1);
+        return 0;
     }
     if (csum && (batch != 1 || trans_b)) {
         fprintf(stderr, "[HIP ERROR] trlm_gemm: column sums need a single GEMM with B stored [K,N]\n");
