@@ -42,6 +42,9 @@ enum { DM_PLAIN = 0, DM_QKV = 1, DM_SWIGLU = 2 };
 #include "../kernel_params.h"   // GemmParams, AttnParams, DecGemmParams
 
 __device__ __forceinline__ f32x4_t ld4(const float* p) { return *(const f32x4_t*)p; }
+// a streamed load (the KV cache is read once per step): the non-temporal hint
+// keeps it from displacing the weights the step's GEMMs re-read from cache
+__device__ __forceinline__ f32x4_t ld4_stream(const float* p) { return __builtin_nontemporal_load((const f32x4_t*)p); }
 
 template <int KW, int RB, bool NT, int MODE, bool NORM>
 __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
@@ -389,8 +392,8 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, int ldq, c
     for (int it = 0; it < NIT; it++) {
         const int j = j0 + it * RPI + sub;
         const long long off = (long long)(j < j1 ? j : 0) * HD;
-        kn[it] = ld4(kb + off);
-        vn[it] = ld4(vb + off);
+        kn[it] = ld4_stream(kb + off);
+        vn[it] = ld4_stream(vb + off);
     }
     for (int p0 = j0; p0 < j1; p0 += PASS) {
         f32x4_t kr[NIT], vr[NIT];
@@ -400,8 +403,8 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, int ldq, c
             vr[it] = vn[it];
             const int j = p0 + PASS + it * RPI + sub;
             const long long off = (long long)(j < j1 ? j : 0) * HD;
-            kn[it] = ld4(kb + off);
-            vn[it] = ld4(vb + off);
+            kn[it] = ld4_stream(kb + off);
+            vn[it] = ld4_stream(vb + off);
         }
         float sc[NIT];
         float pm = -INFINITY;
