@@ -39,6 +39,7 @@ k_cache_fill(const float* __restrict__ qkv, int ldq, int B, int len, int H, int 
 // both as the next step's input ids[row] and into hist[row*hist_ld + step]
 // with step = *pos_dev - pos_base, so generation needs no host round trip.
 #define ARGMAX_THREADS 1024
+#define ARGMAX_UNROLL 8
 extern "C" __global__ void __launch_bounds__(ARGMAX_THREADS)
 k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restrict__ ids,
               unsigned* __restrict__ hist, int hist_ld, const int* __restrict__ pos_dev, int pos_base) {
@@ -51,12 +52,26 @@ k_argmax_hist(const float* __restrict__ logits, int ld, int V, unsigned* __restr
     // each thread scans its float4s in increasing index order, strict > keeps
     // the first occurrence; the reductions prefer the lower index on ties
     if ((ld & 3) == 0) {
+        // ARGMAX_UNROLL float4s per thread in flight at once (loads from
+        // clamped valid addresses first, then the compares in index order)
+        constexpr int U = ARGMAX_UNROLL;
         const int nq = V >> 2;
-        for (int q = threadIdx.x; q < nq; q += ARGMAX_THREADS) {
-            const f32x4 v = *(const f32x4*)(z + 4 * q);
+        for (int q0 = threadIdx.x; q0 < nq; q0 += U * ARGMAX_THREADS) {
+            f32x4 v[U];
 #pragma unroll
-            for (int e = 0; e < 4; e++)
-                if (v[e] > best) { best = v[e]; idx = 4 * q + e; }
+            for (int u = 0; u < U; u++) {
+                const int q = q0 + u * ARGMAX_THREADS;
+                v[u] = *(const f32x4*)(z + 4 * (q < nq ? q : q0));
+            }
+#pragma unroll
+            for (int u = 0; u < U; u++) {
+                const int q = q0 + u * ARGMAX_THREADS;
+                if (q < nq) {
+#pragma unroll
+                    for (int e = 0; e < 4; e++)
+                        if (v[u][e] > best) { best = v[u][e]; idx = 4 * q + e; }
+                }
+            }
         }
         for (int j = 4 * nq + (int)threadIdx.x; j < V; j += ARGMAX_THREADS)
             if (z[j] > best) { best = z[j]; idx = j; }
