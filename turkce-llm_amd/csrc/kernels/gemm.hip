@@ -72,10 +72,22 @@ __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, i
     tn = in / gm;
 }
 
+// K-major tiles keep k contiguous, one row per m/n index.  With BK = 16 a
+// row is 16 floats and its four 16-byte chunks are stored XOR-swizzled by
+// (row/2) % 4: the 8 lanes an LDS cycle serves then touch 32 distinct banks
+// both when a store covers two whole rows and when a fragment read takes one
+// chunk of 8 consecutive rows (a 4-float row pad, the BK = 32 layout, leaves
+// every store 2-way conflicted at BK = 16).
+template <int BK>
+__device__ __forceinline__ int kmajor_slot(int row, int chunk) {
+    if (BK == 16) return row * 16 + 4 * (chunk ^ ((row >> 1) & 3));
+    return row * (BK + 4) + 4 * chunk;
+}
+
 template <int R, int BK, bool KMAJOR>
 struct TileLds {
-    // KMAJOR: [R][BK+4] (k contiguous); else [BK][R] (m/n contiguous)
-    static constexpr int SIZE = KMAJOR ? R * (BK + 4) : BK * R;
+    // KMAJOR: [R][BK] swizzled (BK = 16) or [R][BK+4]; else [BK][R] (m/n contiguous)
+    static constexpr int SIZE = KMAJOR ? R * (BK == 16 ? BK : BK + 4) : BK * R;
 };
 
 // Load one operand tile (R rows of m/n, BK of k) from global memory into
@@ -126,8 +138,8 @@ __device__ __forceinline__ void store_tile(float* lds, const f32x4* regs) {
     for (int i = 0; i < NL; i++) {
         int idx = t + i * 256;
         if (KMAJOR) {
-            int r = idx / (BK / 4), k = (idx % (BK / 4)) * 4;
-            *(f32x4*)(lds + r * (BK + 4) + k) = regs[i];
+            int r = idx / (BK / 4), c = idx % (BK / 4);
+            *(f32x4*)(lds + kmajor_slot<BK>(r, c)) = regs[i];
         } else {
             int k = idx / (R / 4), r = (idx % (R / 4)) * 4;
             *(f32x4*)(lds + k * R + r) = regs[i];
@@ -141,7 +153,7 @@ __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, in
     const int row = rb + (lane & 31);
     const int kq = kk + 4 * (lane >> 5);
     if (KMAJOR) {
-        return *(const f32x4*)(lds + row * (BK + 4) + kq);
+        return *(const f32x4*)(lds + kmajor_slot<BK>(row, kq >> 2));
     } else {
         f32x4 v;
 #pragma unroll
