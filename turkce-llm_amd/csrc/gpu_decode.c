@@ -11,8 +11,9 @@
  *            each sequence only;
  *   step:    one new token per sequence, five fused kernels per layer
  *            (kernels/decode_fused.hip): RMSNorm + QKV + RoPE + cache append;
- *            attention over the cache in 128-key chunks, merged in chunk
- *            order by the last chunk to finish; out-projection + residual;
+ *            attention over the cache, a workgroup per (sequence, head)
+ *            whose 8 waves split the context and merge in wave order;
+ *            out-projection + residual;
  *            RMSNorm + gate/up + SwiGLU; down-projection + residual; then the
  *            final norm + LM head on `batch` rows.  Layer 0 reads its input
  *            rows straight from the embedding table.
