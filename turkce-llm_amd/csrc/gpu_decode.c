@@ -9,11 +9,11 @@
  *            batch x len rows, with a per-layer hook that copies the rotated
  *            K and V into the cache; the LM head runs on the last row of
  *            each sequence only;
- *   step:    one new token per sequence, five fused kernels per layer
- *            (kernels/decode_fused.hip): RMSNorm + QKV + RoPE + cache append;
- *            attention over the cache, a workgroup per (sequence, head)
- *            whose 8 waves split the context and merge in wave order;
- *            out-projection + residual;
+ *   step:    one new token per sequence, four fused kernels per layer
+ *            (kernels/decode_fused.hip): per (sequence, head) a workgroup
+ *            forms the head's RMSNorm + QKV + RoPE, appends k and v to the
+ *            cache and attends over it, its 8 waves splitting the context
+ *            and merging in wave order; out-projection + residual;
  *            RMSNorm + gate/up + SwiGLU; down-projection + residual; then the
  *            final norm + LM head on `batch` rows.  Layer 0 reads its input
  *            rows straight from the embedding table.
@@ -48,14 +48,14 @@ struct TrlmDecoder {
     hipDeviceptr_t kc, vc;              /* [L][B][H][ctx][hd] each */
     hipDeviceptr_t cos_t, sin_t;        /* [ctx][hd/2] */
     /* step buffers, B rows */
-    hipDeviceptr_t ids, x, x2, qkv, att, h, nf, logits, out_ids;
+    hipDeviceptr_t ids, x, x2, att, h, nf, logits, out_ids;
     /* sampling scratch */
     hipDeviceptr_t e, prefix, u;
     /* prefill buffers, grown to batch x len rows on demand */
     u64 pre_rows;
     hipDeviceptr_t p_x, p_x2, p_n, p_r1, p_r2, p_qkv, p_att, p_lse, p_gu, p_h, p_nf, p_rf, p_ids;
     hipFunction_t k_fill, k_gather, k_sample, k_argmax_hist;
-    hipFunction_t k_qkv, k_out, k_gu, k_down, k_head, k_attn;
+    hipFunction_t k_qkv_attn, k_out, k_gu, k_down, k_head;
     /* step replay: the position lives on the device (pos_dev), so every step
      * is the same launch sequence -- captured once as a HIP graph on the
      * second step */
@@ -104,7 +104,6 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->ids = hip_alloc(B * sizeof(u32));
     d->x = fl(B * D);
     d->x2 = fl(B * D);
-    d->qkv = fl(B * D);   /* the step's rotated queries */
     d->att = fl(B * D);
     d->h = fl(B * F);
     d->nf = fl(B * D);
@@ -144,13 +143,12 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->k_gather = hip_get_kernel(c, "k_gather_rows");
     d->k_sample = hip_get_kernel(c, "k_sample_rows");
     d->k_argmax_hist = hip_get_kernel(c, "k_argmax_hist");
-    d->k_qkv = hip_get_kernel(c, "k_dec_qkv");
     d->k_out = hip_get_kernel(c, "k_dec_out");
     d->k_gu = hip_get_kernel(c, "k_dec_gu");
     d->k_down = hip_get_kernel(c, "k_dec_down");
     d->k_head = hip_get_kernel(c, "k_dec_head");
-    snprintf(name, sizeof(name), "k_dec_attn_hd%u", g->hd);
-    d->k_attn = hip_get_kernel(c, name);
+    snprintf(name, sizeof(name), "k_dec_qkv_attn_hd%u", g->hd);
+    d->k_qkv_attn = hip_get_kernel(c, name);
     d->pos_dev = hip_alloc(sizeof(i32));
     hip_sync();
     return d;
@@ -177,7 +175,7 @@ void gpu_decoder_destroy(TrlmDecoder* d) {
     free_prefill(d);
     if (d->hist) hip_free(d->hist);
     hip_free(d->pos_dev);
-    hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->qkv, d->att, d->h, d->nf,
+    hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->att, d->h, d->nf,
                               d->logits, d->out_ids, d->e, d->prefix, d->u, d->cos_t, d->sin_t };
     for (u32 i = 0; i < sizeof(bufs) / sizeof(bufs[0]); i++) hip_free(bufs[i]);
     free(d);
@@ -283,7 +281,7 @@ static void step_body(TrlmDecoder* d) {
     const i32 Bc = (i32)d->B, D = (i32)d->D, F = (i32)d->F, H = (i32)d->H, hd = (i32)d->hd, ctxn = (i32)d->ctx;
     const float* E = (const float*)trlm_param_ptr(g, 0);
     const u64 per_layer = (u64)d->B * d->H * d->ctx * d->hd;
-    hipDeviceptr_t x = d->x, x2 = d->x2, q = d->qkv, att = d->att, h = d->h, logits = d->logits, posd = d->pos_dev;
+    hipDeviceptr_t x = d->x, x2 = d->x2, att = d->att, h = d->h, logits = d->logits, posd = d->pos_dev;
     DecGemmParams base;
     memset(&base, 0, sizeof(base));
     base.E = E;
@@ -298,20 +296,18 @@ static void step_body(TrlmDecoder* d) {
 #define PP(k) ((const float*)trlm_param_ptr(g, trlm_pidx(l, k)))
         float* kc = (float*)at(d->kc, l * per_layer);
         float* vc = (float*)at(d->vc, l * per_layer);
-        /* q | k -> cache | v -> cache = RoPE(RMSNorm(x) @ Wqkv + b) */
+        /* per (sequence, head): q | k -> cache | v -> cache = RoPE(RMSNorm(x) @ Wqkv + b),
+         * then att = the attention of q over the cache and the new key */
         DecGemmParams p = base;
         p.A = (const float*)x; p.a_ids = l == 0; p.lda = D;
         p.W = PP(PK_WQKV); p.ldw = 3 * D; p.bias = PP(PK_BQKV); p.norm_w = PP(PK_ATTN_NORM);
-        p.C = (float*)q; p.ldc = D;
-        p.N = 3 * D; p.K = D; p.ncb = (i32)cdiv32((u64)(3 * D), 16);
+        p.C = (float*)att; p.ldc = D;
+        p.N = 3 * D; p.K = D;
         p.kc = kc; p.vc = vc;
-        dec_gemm_launch(d->k_qkv, &p, 1, 4);
+        p.scale = d->scale;
         {
-            hipDeviceptr_t kcp = kc, vcp = vc;
-            i32 ldq = D;
-            f32 scale = d->scale;
-            void* args[] = { &q, &ldq, &kcp, &vcp, &posd, (void*)&ctxn, (void*)&H, &scale, &att, (void*)&D };
-            hip_launch(d->k_attn, (u32)Bc * d->H, 1, 1, 64 * DEC_ATT_WAVES, 1, 1, 0, args);
+            void* args[] = { &p };
+            hip_launch(d->k_qkv_attn, (u32)Bc * d->H, 1, 1, 64 * DEC_ATT_WAVES, 1, 1, 0, args);
         }
         /* x2 = x + (att @ Wo + bo) */
         p = base;

@@ -85,6 +85,7 @@ typedef struct DecGemmParams {
     float* vc;
     int ctx;
     int* pos_inc;            // head: block 0 adds 1 to *pos_inc after its stores
+    float scale;             // QKV + attention: the score scale 1/sqrt(hd)
 } DecGemmParams;
 
 #endif /* TRLM_KERNEL_PARAMS_H */

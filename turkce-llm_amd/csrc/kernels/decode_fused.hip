@@ -1,14 +1,15 @@
-// decode_fused.hip -- the KV-cache decode step as five kernels per layer.
+// decode_fused.hip -- the KV-cache decode step as four kernels per layer.
 //
 // A decode step runs the model on one new token per sequence: every product
 // has only `batch` rows (64 in the benchmark), so the step is bound by
 // latency and HBM, not by the matrix cores.  The reference computes it as
 // the full-window lm_forward (training/generate.c:186-212); within the
 // context the last row needs only the cached keys and values, so a step is:
-//   k_dec_qkv   RMSNorm(x) @ Wqkv + b, RoPE on q and k at the position,
-//               k and v appended to the cache, q kept       (layer 0: x = E[ids])
-//   k_dec_attn  q over the cached keys: a workgroup per (sequence, head),
-//               its 8 waves splitting the context, merged in wave order
+//   k_dec_qkv_attn  per (sequence, head): RMSNorm(x) @ Wqkv + b for the
+//               head's columns, RoPE on q and k at the position, k and v
+//               appended to the cache, then q over the cached keys and the
+//               new one, the 8 waves splitting the context, merged in wave
+//               order                                  (layer 0: x = E[ids])
 //   k_dec_out   x2 = x + (att @ Wo + bo)
 //   k_dec_gu    h = SwiGLU(RMSNorm(x2) @ Wgu + bgu)
 //   k_dec_down  x = x2 + (h @ Wd + bd)
@@ -35,7 +36,7 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 #define DEC_LOG2E_F 1.4426950408889634f
 
-enum { DM_PLAIN = 0, DM_QKV = 1, DM_SWIGLU = 2 };
+enum { DM_PLAIN = 0, DM_SWIGLU = 2 };
 
 // Argument block of the fused GEMMs; layout mirrored by DecGemmParams in
 // gpu_decode.c.
@@ -88,10 +89,8 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
     if (NACC == 2) bcol[NACC - 1] = cvalid ? p.F + c : 0;
 
     // wave 0's epilogue inputs, loaded now so they arrive with the operands:
-    // bias, residual rows (this lane's 4 rows per row block), and for the
-    // QKV epilogue the position and this lane's RoPE pair
-    float ebias[NACC], eres[RB][4], ecs = 1.f, esn = 0.f;
-    int pos = 0;
+    // bias and residual rows (this lane's 4 rows per row block)
+    float ebias[NACC], eres[RB][4];
     if (w == 0) {
 #pragma unroll
         for (int a = 0; a < NACC; a++) ebias[a] = p.bias ? p.bias[bcol[a]] : 0.f;
@@ -107,12 +106,6 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
                                               : p.resid[(long long)m * p.ldr + bcol[0]];
                 }
             }
-        if (MODE == DM_QKV) {
-            pos = *p.pos;
-            const int dcol = c - (c / p.D) * p.D, d = dcol % p.hd, half = p.hd >> 1;
-            ecs = p.cos_t[pos * half + (d >> 1)];
-            esn = p.sin_t[pos * half + (d >> 1)];
-        }
     }
 
     f32x4_t acc[RB][NACC];
@@ -226,22 +219,7 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
             float o[NACC];
 #pragma unroll
             for (int a = 0; a < NACC; a++) o[a] = v[a][r] * scale + ebias[a];
-            if (MODE == DM_QKV) {
-                // columns of q | k | v; RoPE pairs (2k, 2k+1) are neighbouring lanes
-                const float partner = __shfl_xor(o[0], 1, WAVE);
-                const int reg = c / p.D, dcol = c - reg * p.D;
-                const int h = dcol / p.hd, d = dcol - h * p.hd;
-                float val = o[0];
-                if (reg < 2) val = (d & 1) ? partner * esn + o[0] * ecs : o[0] * ecs - partner * esn;
-                if (m < p.M && cvalid) {
-                    if (reg == 0) {
-                        p.C[(long long)m * p.ldc + dcol] = val;
-                    } else {
-                        float* cache = reg == 1 ? p.kc : p.vc;
-                        cache[(((long long)m * p.H + h) * p.ctx + pos) * p.hd + d] = val;
-                    }
-                }
-            } else if (MODE == DM_SWIGLU) {
+            if (MODE == DM_SWIGLU) {
                 const float g = o[0], u = o[NACC - 1];
                 const float sg = 1.0f / (1.0f + expf(-g));
                 if (m < p.M && cvalid) p.C[(long long)m * p.ldc + c] = (g * sg) * u;
@@ -253,7 +231,6 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
     if (p.pos_inc && blockIdx.x == 0 && threadIdx.x == 0) *p.pos_inc = *p.pos_inc + 1;
 }
 
-extern "C" __global__ void __launch_bounds__(256) k_dec_qkv(DecGemmParams p) { dec_gemm<4, 1, false, DM_QKV, true>(p); }
 extern "C" __global__ void __launch_bounds__(256) k_dec_out(DecGemmParams p) { dec_gemm<4, 1, false, DM_PLAIN, false>(p); }
 extern "C" __global__ void __launch_bounds__(256) k_dec_gu(DecGemmParams p) { dec_gemm<4, 1, false, DM_SWIGLU, true>(p); }
 extern "C" __global__ void __launch_bounds__(512) k_dec_down(DecGemmParams p) { dec_gemm<8, 1, false, DM_PLAIN, false>(p); }
@@ -354,47 +331,23 @@ extern "C" __global__ void __launch_bounds__(64 * DEC_HEAD_WAVES) k_dec_head(Dec
 }
 
 // ---------------------------------------------------------------- attention
-// One workgroup of 8 waves per (sequence b, head h), for the query
-// q[b, h*HD ..] over the n = *pos + 1 cached keys.  Wave w takes the keys
-// [w*per, (w+1)*per) and walks them in passes of 8*RPI rows, with an online
-// softmax (base-2 running max, rescaled sum and O); lanes work in groups of
-// LPR = HD/4 lanes per key row (float4 each, whole rows per wave
-// instruction), and a pass's K and V rows are all loaded before any
-// arithmetic.  The 8 waves' (max, sum, O) are merged through LDS in wave
-// order, so the result is deterministic; no workgroup waits for another.
-#define DEC_ATT_WAVES 8
-template <int HD, int WAVES = DEC_ATT_WAVES, int NIT = 4>
-__device__ __forceinline__ void dec_attn(const float* __restrict__ q, int ldq, const float* __restrict__ kc,
-                                         const float* __restrict__ vc, const int* __restrict__ pos_dev, int ctx,
-                                         int H, float scale, float* __restrict__ att, int D) {
+// One wave's share of a decode attention: q (this lane's 4 components, LPR =
+// HD/4 lanes per key row) over the cached key rows [j0, j1) of one (sequence,
+// head), with an online softmax in base 2.  The wave walks its rows in passes
+// of NIT*RPI; kn / vn hold the first pass's rows, loaded by the caller
+// (unconditionally, from rows clamped to row 0, which always holds a key), and
+// every pass loads the next one's before its arithmetic.  Returns the wave's
+// running max (-inf without keys), its sum of exponentials and its O (the
+// wave's row groups added), the same in every lane of a column quad.
+template <int HD, int NIT>
+__device__ __forceinline__ void dec_attn_range(const f32x4_t qv, const float* __restrict__ kb,
+                                               const float* __restrict__ vb, int j0, int j1, int sub, float c2,
+                                               f32x4_t (&kn)[NIT], f32x4_t (&vn)[NIT], float& mx_out,
+                                               float& l_out, f32x4_t& o_out) {
     constexpr int LPR = HD / 4, RPI = 64 / LPR, PASS = NIT * RPI;
-    __shared__ float wm[WAVES], wl[WAVES];
-    __shared__ f32x4_t wo[WAVES][LPR];
-    const int n = *pos_dev + 1;
-    const int bh = blockIdx.x, b = bh / H, h = bh - b * H;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const int sub = lane / LPR, c4 = lane % LPR;
-    const int per = ((n + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;
-    const int j0 = wave * per;
-    int j1 = j0 + per;
-    if (j1 > n) j1 = n;
-    const float c2 = scale * DEC_LOG2E_F;
-    const float* kb = kc + (long long)bh * ctx * HD + 4 * c4;
-    const float* vb = vc + (long long)bh * ctx * HD + 4 * c4;
-    const f32x4_t qv = ld4(q + (long long)b * ldq + h * HD + 4 * c4);
-
+    const int c4 = (threadIdx.x & 63) % LPR;
     float mx = -INFINITY, ls = 0.f;
     f32x4_t o = {0.f, 0.f, 0.f, 0.f};
-    // pass p's rows are loaded during pass p-1's arithmetic; loads are
-    // unconditional, from clamped rows (row 0 always holds a key)
-    f32x4_t kn[NIT], vn[NIT];
-#pragma unroll
-    for (int it = 0; it < NIT; it++) {
-        const int j = j0 + it * RPI + sub;
-        const long long off = (long long)(j < j1 ? j : 0) * HD;
-        kn[it] = ld4_stream(kb + off);
-        vn[it] = ld4_stream(vb + off);
-    }
     for (int p0 = j0; p0 < j1; p0 += PASS) {
         f32x4_t kr[NIT], vr[NIT];
 #pragma unroll
@@ -441,34 +394,194 @@ __device__ __forceinline__ void dec_attn(const float* __restrict__ q, int ldq, c
         o[2] += __shfl_xor(o[2], sh, WAVE);
         o[3] += __shfl_xor(o[3], sh, WAVE);
     }
+    mx_out = mx;
+    l_out = lrow;
+    o_out = o;
+}
+
+#define DEC_ATT_WAVES 8
+
+// ------------------------------------------------- QKV projection + attention
+// One workgroup of 8 waves per (sequence b, head h) computes the head's q, k
+// and v of the new token itself -- RMSNorm(x[b]) @ Wqkv[:, head columns] + b,
+// RoPE on q and k at the position -- appends k and v to the cache, and runs
+// the attention of q over the cached keys 0 .. pos-1 (each wave a
+// contiguous range, dec_attn_range) and the new key, merged in wave order
+// with the new key last.  This removes the step's separate QKV kernel and its boundary: every
+// input of a head's attention is the row x[b] and a 3*HD-column slice of
+// Wqkv (the workgroups of a head read the same slice from cache).
+//
+// Projection: wave w takes rows [w*rw, (w+1)*rw) of the slice; lane
+// (sub, c4) reads W[k][seg*D + h*HD + 4c4 .. +3] of the three segments for
+// rows k = k0 + RPI*g + sub, so one wave instruction covers RPI whole rows of
+// a segment.  The normalisation is applied after the sum,
+// out = r * sum_k (x[k] w[k]) W[k][c] + bias, r = 1/sqrt(mean(x^2) + eps) in
+// f64 as in k_rmsnorm_fwd.  The per-row values x[k] w[k] reach the lanes by
+// lane shuffles, and the partial sums go through LDS to wave 0, which adds
+// them in wave order.  The first pass of the cache stream is issued before
+// the projection (it does not depend on q), so it is in flight meanwhile.
+template <int HD, int WAVES = DEC_ATT_WAVES, int NIT = 4>
+__device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
+    constexpr int LPR = HD / 4, RPI = 64 / LPR, PASS = NIT * RPI;
+    constexpr int GB = 4;                       // row groups per load batch of the projection
+    __shared__ f32x4_t red[WAVES][3][LPR];      // the waves' partial q | k | v sums
+    __shared__ f32x4_t hv[3][LPR];              // the head's q, new k, new v
+    __shared__ float wm[WAVES], wl[WAVES];
+    __shared__ f32x4_t wo[WAVES][LPR];
+    __shared__ float s_new;
+    const int pos = *p.pos;                     // the new token's position = cached keys
+    // consecutive workgroups take different heads, so the workgroups on one
+    // XCD (every 8th) read only a few of the heads' Wqkv slices
+    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sub = lane / LPR, c4 = lane % LPR;
+    const int D = p.D;
+    const float c2 = p.scale * DEC_LOG2E_F;
+
+    // this wave's cached keys and its first pass's loads (clamped to row 0,
+    // which the prefill always wrote; rows past the wave's keys weigh 0)
+    const int n = pos;
+    const int per = ((n + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;
+    const int j0 = wave * per;
+    int j1 = j0 + per;
+    if (j1 > n) j1 = n;
+    const long long head_rows = (long long)bh * p.ctx;
+    const float* kb = p.kc + head_rows * HD + 4 * c4;
+    const float* vb = p.vc + head_rows * HD + 4 * c4;
+    f32x4_t kn[NIT], vn[NIT];
+#pragma unroll
+    for (int it = 0; it < NIT; it++) {
+        const int j = j0 + it * RPI + sub;
+        const long long off = (long long)(j < j1 ? j : 0) * HD;
+        kn[it] = ld4_stream(kb + off);
+        vn[it] = ld4_stream(vb + off);
+    }
+
+    // ---- projection of x[b] onto the head's q | k | v columns
+    const float* xr = p.a_ids ? p.E + (long long)p.ids[b] * p.lda : p.A + (long long)b * p.lda;
+    const int rw = ((D + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;   // rows per wave (<= 64 for D <= 512)
+    const int k0 = wave * rw;
+    int k1 = k0 + rw;
+    if (k1 > D) k1 = D;
+    // lane i < rw holds x[k0 + i] * w[k0 + i]
+    float xw;
+    {
+        const int k = k0 + lane;
+        const int ks = k < k1 ? k : 0;
+        const float xv = xr[ks], wv = p.norm_w[ks];
+        xw = (k < k1 && lane < rw) ? xv * wv : 0.f;
+    }
+    // wave 0 also forms the row's sum of squares for r
+    float ss = 0.f;
+    if (wave == 0) {
+        for (int q4 = lane; q4 < D / 4; q4 += 64) {
+            const f32x4_t v = ld4(xr + 4 * q4);
+            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
+        }
+        ss = wave_sum(ss);
+    }
+    const float* wcol = p.W + h * HD + 4 * c4;   // q column quad; k at + D, v at + 2D
+    f32x4_t acc[3];
+#pragma unroll
+    for (int s = 0; s < 3; s++) acc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int g0 = 0; g0 < rw; g0 += GB * RPI) {
+        f32x4_t wv[GB][3];
+#pragma unroll
+        for (int j = 0; j < GB; j++) {
+            const int k = k0 + g0 + j * RPI + sub;
+            const long long ks = k < k1 ? k : 0;
+#pragma unroll
+            for (int s = 0; s < 3; s++) wv[j][s] = ld4(wcol + ks * p.ldw + s * D);
+        }
+#pragma unroll
+        for (int j = 0; j < GB; j++) {
+            const int i = g0 + j * RPI + sub;           // row offset inside the wave's range
+            const float xk = __shfl(xw, i < 64 ? i : 63, WAVE);
+            const bool kv = i < rw && k0 + i < k1;
+#pragma unroll
+            for (int s = 0; s < 3; s++) acc[s] += (kv ? xk : 0.f) * wv[j][s];
+        }
+    }
+    // rows of the wave -> one partial per column quad
+#pragma unroll
+    for (int sh = LPR; sh < 64; sh <<= 1)
+#pragma unroll
+        for (int s = 0; s < 3; s++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) acc[s][e] += __shfl_xor(acc[s][e], sh, WAVE);
+    if (sub == 0) {
+#pragma unroll
+        for (int s = 0; s < 3; s++) red[wave][s][c4] = acc[s];
+    }
+    __syncthreads();
+    if (wave == 0 && lane < 3 * LPR) {
+        const int s = lane / LPR, cq = lane % LPR;
+        f32x4_t y = red[0][s][cq];
+#pragma unroll
+        for (int w = 1; w < WAVES; w++) y += red[w][s][cq];
+        const float r = 1.0f / (float)sqrt((double)(ss / (float)D + p.eps));
+        const f32x4_t bv = ld4(p.bias + s * D + h * HD + 4 * cq);
+#pragma unroll
+        for (int e = 0; e < 4; e++) y[e] = y[e] * r + bv[e];
+        if (s < 2) {
+            // RoPE on the pairs (4cq, 4cq+1) and (4cq+2, 4cq+3)
+#pragma unroll
+            for (int i = 0; i < 2; i++) {
+                const int t = pos * (HD / 2) + 2 * cq + i;
+                const float cs = p.cos_t[t], sn = p.sin_t[t];
+                const float ye = y[2 * i], yo = y[2 * i + 1];
+                y[2 * i] = ye * cs - yo * sn;
+                y[2 * i + 1] = ye * sn + yo * cs;
+            }
+        }
+        hv[s][cq] = y;
+        if (s > 0) *(f32x4_t*)((s == 1 ? p.kc : p.vc) + (head_rows + pos) * HD + 4 * cq) = y;
+    }
+    __syncthreads();
+    const f32x4_t qv = hv[0][c4];
+    if (wave == 0) {
+        // the new key's score, formed as the cached keys' scores are
+        const f32x4_t kv = hv[1][c4];
+        float d = kv[0] * qv[0] + kv[1] * qv[1] + kv[2] * qv[2] + kv[3] * qv[3];
+#pragma unroll
+        for (int sh = 1; sh < LPR; sh <<= 1) d += __shfl_xor(d, sh, WAVE);
+        if (lane == 0) s_new = d * c2;
+    }
+
+    // ---- attention over the cached keys, merged with the new key
+    float mx, lrow;
+    f32x4_t o;
+    dec_attn_range<HD, NIT>(qv, kb, vb, j0, j1, sub, c2, kn, vn, mx, lrow, o);
     if (sub == 0) wo[wave][c4] = o;
     if (lane == 0) { wm[wave] = mx; wl[wave] = lrow; }
     __syncthreads();
     if (threadIdx.x < LPR) {
-        float M = -INFINITY;
+        const float sn = s_new;
+        float M = sn;
 #pragma unroll
         for (int w = 0; w < WAVES; w++) M = fmaxf(M, wm[w]);
         float L = 0.f;
-        f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int w = 0; w < WAVES; w++) {
             const float wt = wm[w] == -INFINITY ? 0.f : exp2f(wm[w] - M);   // waves without keys weigh 0
             L += wt * wl[w];
-            acc += wt * wo[w][threadIdx.x];
+            a += wt * wo[w][threadIdx.x];
         }
-        *(f32x4_t*)(att + (long long)b * D + h * HD + 4 * threadIdx.x) = acc / L;
+        const float wt = exp2f(sn - M);
+        L += wt;
+        a += wt * hv[2][threadIdx.x];
+        *(f32x4_t*)(p.C + (long long)b * p.ldc + h * HD + 4 * threadIdx.x) = a / L;
     }
 }
 
-#define DEC_ATTN_KERNEL(HD)                                                                                   \
-    extern "C" __global__ void __launch_bounds__(64 * DEC_ATT_WAVES)                                          \
-    k_dec_attn_hd##HD(const float* q, int ldq, const float* kc, const float* vc, const int* pos_dev, int ctx, \
-                      int H, float scale, float* att, int D) {                                                \
-        dec_attn<HD>(q, ldq, kc, vc, pos_dev, ctx, H, scale, att, D);                                         \
+#define DEC_QKV_ATTN_KERNEL(HD)                                                                               \
+    extern "C" __global__ void __launch_bounds__(64 * DEC_ATT_WAVES) k_dec_qkv_attn_hd##HD(DecGemmParams p) { \
+        dec_qkv_attn<HD>(p);                                                                                  \
     }
-DEC_ATTN_KERNEL(16)
-DEC_ATTN_KERNEL(32)
-DEC_ATTN_KERNEL(64)
+DEC_QKV_ATTN_KERNEL(16)
+DEC_QKV_ATTN_KERNEL(32)
+DEC_QKV_ATTN_KERNEL(64)
 
 // Lane layout of v_mfma_f32_16x16x4f32 (checked exactly by a test):
 // out[lane*4 + r] = result register r of lane `lane`.
