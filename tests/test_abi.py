@@ -119,7 +119,7 @@ def test_code_object_has_every_kernel(trlm):
     names |= {"k_attn_fwd_hd%d" % d for d in (16, 32, 64)} | {"k_attn_bwd_dq_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_dvec_hd%d" % d for d in (16, 32, 64)}
     names |= {"k_attn_bwd_dkv_hd%d" % d for d in (16, 32, 64)}
-    names |= {"k_dec_qkv_attn_hd%d" % d for d in (16, 32, 64)}
+    names |= {"k_dec_qkv_attn_hd%d" % d for d in (16, 32, 64)} | {"k_dec_head_k%d" % n for n in (8, 24, 32)}
     names |= {"k_gemm_%s_%s" % (l, t) for l in ("nn", "nt", "tn") for t in (
         "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32")}
     names |= {"k_gemm_%s_64x64_u" % l for l in ("nn", "nt", "tn", "tt")} | {"k_gemm_nn_64x64_k32_glu"}
@@ -160,11 +160,11 @@ def test_kernel_argument_blocks_match_host_structs(trlm, tmp_path):
             want[n] = gemm
         elif re.match(r"k_attn_(fwd|bwd_dkv|bwd_dq|dvec)_hd\d+$", n):
             want[n] = attn
-        elif n in ("k_dec_out", "k_dec_gu", "k_dec_down", "k_dec_head") or re.match(r"k_dec_qkv_attn_hd\d+$", n):
+        elif n in ("k_dec_out", "k_dec_gu", "k_dec_down") or re.match(r"k_dec_(qkv_attn_hd|head_k)\d+$", n):
             want[n] = dec
     assert len([n for n in want if n.startswith("k_gemm_")]) == 29   # 8 tiles x 3 layouts, 4 unaligned, SwiGLU
     assert len([n for n in want if n.startswith("k_attn_")]) == 12
-    assert len([n for n in want if n.startswith("k_dec_")]) == 7   # out, gu, down, head, QKV + attention x 3
+    assert len([n for n in want if n.startswith("k_dec_")]) == 9   # out, gu, down, head x 3, QKV + attention x 3
     for k in kernels:
         n = k[".name"]
         if n not in want:

@@ -146,7 +146,9 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->k_out = hip_get_kernel(c, "k_dec_out");
     d->k_gu = hip_get_kernel(c, "k_dec_gu");
     d->k_down = hip_get_kernel(c, "k_dec_down");
-    d->k_head = hip_get_kernel(c, "k_dec_head");
+    /* the LM head holds a whole 16-column block of E in registers: the
+     * instantiation with the fewest 16-deep steps covering d_model */
+    d->k_head = hip_get_kernel(c, g->D <= 128 ? "k_dec_head_k8" : g->D <= 384 ? "k_dec_head_k24" : "k_dec_head_k32");
     snprintf(name, sizeof(name), "k_dec_qkv_attn_hd%u", g->hd);
     d->k_qkv_attn = hip_get_kernel(c, name);
     d->pos_dev = hip_alloc(sizeof(i32));

@@ -238,86 +238,101 @@ extern "C" __global__ void __launch_bounds__(512) k_dec_down(DecGemmParams p) { 
 // ---------------------------------------------------------------- LM head
 // logits[m, n] = sum_k (x[m, k] r[m] w[k]) E[n, k] for the (up to) 64 rows of
 // row tile blockIdx.y, with r the row's RMSNorm reciprocal.  A persistent
-// grid: each workgroup first writes its rows' normalised values
-// (x * r * w, elementwise as the reference's norm) into LDS, once; then each
-// of its 8 waves walks column blocks of 16 vocabulary rows over the whole of
-// K, four 16-row MFMA blocks sharing every E fragment, with the next 64-deep
-// chunk of E loaded while the current one's 64 MFMAs issue.  LDS rows are
-// padded by 4 floats so the 16 rows of a fragment read fall in different
-// banks.  K <= DEC_HEAD_KMAX, K % 16 == 0.
+// grid of 8-wave workgroups, wave w of workgroup g taking the 16-column
+// blocks of E g*8 + w, g*8 + w + 8*grid, ...  Every wave first issues all its
+// loads: its 8 rows of x, then the whole first column block of E (NKB
+// 16-deep steps, one f32x4 per lane each), so the E stream has the block in
+// flight while the rows are normalised into LDS (x was issued first, so the
+// in-order memory counter lets the staging start before E arrives).  Then
+// four 16-row MFMA blocks share every E fragment.  LDS rows are padded by 4
+// floats so the 16 rows of a fragment read fall in different banks.
+// K <= 16*NKB <= DEC_HEAD_KMAX, K % 16 == 0.
 #define DEC_HEAD_KMAX 512
 #define DEC_HEAD_WAVES 8
-extern "C" __global__ void __launch_bounds__(64 * DEC_HEAD_WAVES) k_dec_head(DecGemmParams p) {
+template <int NKB>
+__device__ __forceinline__ void dec_head(const DecGemmParams& p) {
     constexpr int LDK = DEC_HEAD_KMAX + 4;
+    constexpr int RPW = 64 / DEC_HEAD_WAVES;   // rows staged per wave
     __shared__ float xs[64 * LDK];
-    __shared__ float rs[64];
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
     const int li = lane & 15, kq = lane >> 4;
     const int m0 = blockIdx.y * 64;
-    const int K = p.K, K4 = K >> 2;
-    // rows m0 .. m0+63 (clamped) -> sums of squares: wave w takes rows w, w+8, ...
-    for (int rr = w; rr < 64; rr += DEC_HEAD_WAVES) {
-        int m = m0 + rr;
+    const int K = p.K, K4 = K >> 2;   // K4 <= 128: two float4 per lane and row
+    const int nwaves = gridDim.x * DEC_HEAD_WAVES;
+
+    // this wave's rows w, w + 8, ... and the norm weight (clamped loads)
+    f32x4_t xv[RPW][2], nw[2];
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
+        int m = m0 + w + DEC_HEAD_WAVES * r;
         if (m > p.M - 1) m = p.M - 1;
         const float* xr = p.a_ids ? p.E + (long long)p.ids[m] * p.lda : p.A + (long long)m * p.lda;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const int q = lane + 64 * t;
+            xv[r][t] = ld4(xr + 4 * (q < K4 ? q : 0));
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < 2; t++) {
+        const int q = lane + 64 * t;
+        nw[t] = ld4(p.norm_w + 4 * (q < K4 ? q : 0));
+    }
+    // the first column block of E, whole (steps past K load step 0 and are skipped)
+    int cb = blockIdx.x * DEC_HEAD_WAVES + w;
+    f32x4_t ev[NKB];
+    auto eload = [&](int blk) {
+        int c = 16 * blk + li;
+        if (c > p.N - 1) c = p.N - 1;
+        const float* er = p.W + (long long)c * p.ldw + 4 * kq;
+#pragma unroll
+        for (int j = 0; j < NKB; j++) ev[j] = ld4(er + (16 * j < K ? 16 * j : 0));
+    };
+    eload(cb < p.ncb ? cb : 0);
+
+    // rows -> r = 1/sqrt(mean(x^2) + eps) in f64 -> x * r * w into LDS
+#pragma unroll
+    for (int r = 0; r < RPW; r++) {
         float ss = 0.f;
-        for (int q = lane; q < K4; q += 64) {
-            const f32x4_t v = ld4(xr + 4 * q);
-            ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
-            *(f32x4_t*)(xs + rr * LDK + 4 * q) = v;
+#pragma unroll
+        for (int t = 0; t < 2; t++) {
+            const f32x4_t v = xv[r][t];
+            if (lane + 64 * t < K4) ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         }
         ss = wave_sum(ss);
-        if (lane == 0) rs[rr] = 1.0f / (float)sqrt((double)(ss / (float)K + p.eps));
-    }
-    __syncthreads();
-    for (int i = threadIdx.x; i < 64 * K4; i += 64 * DEC_HEAD_WAVES) {
-        const int rr = i / K4, q = i - rr * K4;
-        const f32x4_t wv = ld4(p.norm_w + 4 * q);
-        f32x4_t v = *(f32x4_t*)(xs + rr * LDK + 4 * q);
-        const float r = rs[rr];
+        const float rr = 1.0f / (float)sqrt((double)(ss / (float)K + p.eps));
+        const int row = w + DEC_HEAD_WAVES * r;
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[e] = v[e] * r * wv[e];
-        *(f32x4_t*)(xs + rr * LDK + 4 * q) = v;
+        for (int t = 0; t < 2; t++) {
+            const int q = lane + 64 * t;
+            if (q < K4) {
+                f32x4_t v = xv[r][t];
+#pragma unroll
+                for (int e = 0; e < 4; e++) v[e] = v[e] * rr * nw[t][e];
+                *(f32x4_t*)(xs + row * LDK + 4 * q) = v;
+            }
+        }
     }
     __syncthreads();
 
-    const int nwaves = gridDim.x * DEC_HEAD_WAVES;
-    for (int cb = blockIdx.x * DEC_HEAD_WAVES + w; cb < p.ncb; cb += nwaves) {
-        const int c = 16 * cb + li;
-        const bool cvalid = c < p.N;
-        const float* er = p.W + (long long)(cvalid ? c : 0) * p.ldw + 4 * kq;
+    for (; cb < p.ncb; cb += nwaves) {
         f32x4_t acc[4];
 #pragma unroll
         for (int rb = 0; rb < 4; rb++) acc[rb] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-        // 16-deep steps past K (K % 16 == 0) load a valid k step and are skipped
-        f32x4_t bn[4];
 #pragma unroll
-        for (int j = 0; j < 4; j++) bn[j] = ld4(er + (16 * j < K ? 16 * j : 0));
-        for (int k0 = 0; k0 < K; k0 += 64) {
-            f32x4_t bv[4];
+        for (int j = 0; j < NKB; j++) {
+            if (16 * j >= K) break;
+            f32x4_t av[4];
 #pragma unroll
-            for (int j = 0; j < 4; j++) bv[j] = bn[j];
-            if (k0 + 64 < K) {
+            for (int rb = 0; rb < 4; rb++) av[rb] = *(const f32x4_t*)(xs + (16 * rb + li) * LDK + 16 * j + 4 * kq);
 #pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const int kn = k0 + 64 + 16 * j;
-                    bn[j] = ld4(er + (kn < K ? kn : 0));
-                }
-            }
+            for (int u = 0; u < 4; u++)
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                if (k0 + 16 * j >= K) break;
-                f32x4_t av[4];
-#pragma unroll
-                for (int rb = 0; rb < 4; rb++) av[rb] = *(const f32x4_t*)(xs + (16 * rb + li) * LDK + k0 + 16 * j + 4 * kq);
-#pragma unroll
-                for (int u = 0; u < 4; u++)
-#pragma unroll
-                    for (int rb = 0; rb < 4; rb++)
-                        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb][u], bv[j][u], acc[rb], 0, 0, 0);
-            }
+                for (int rb = 0; rb < 4; rb++)
+                    acc[rb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[rb][u], ev[j][u], acc[rb], 0, 0, 0);
         }
-        if (cvalid) {
+        const int c = 16 * cb + li;
+        if (c < p.N) {
 #pragma unroll
             for (int rb = 0; rb < 4; rb++)
 #pragma unroll
@@ -326,9 +341,19 @@ extern "C" __global__ void __launch_bounds__(64 * DEC_HEAD_WAVES) k_dec_head(Dec
                     if (m < p.M) p.C[(long long)m * p.ldc + c] = acc[rb][r];
                 }
         }
+        if (cb + nwaves < p.ncb) eload(cb + nwaves);
     }
     if (p.pos_inc && blockIdx.x == 0 && blockIdx.y == 0 && threadIdx.x == 0) *p.pos_inc = *p.pos_inc + 1;
 }
+
+// instantiations by the number of 16-deep steps the register block holds
+#define DEC_HEAD_KERNEL(NKB)                                                                              \
+    extern "C" __global__ void __launch_bounds__(64 * DEC_HEAD_WAVES) k_dec_head_k##NKB(DecGemmParams p) { \
+        dec_head<NKB>(p);                                                                                 \
+    }
+DEC_HEAD_KERNEL(8)
+DEC_HEAD_KERNEL(24)
+DEC_HEAD_KERNEL(32)
 
 // ---------------------------------------------------------------- attention
 // One wave's share of a decode attention: q (this lane's 4 components, LPR =
