@@ -34,7 +34,8 @@
 #include "gpu_internal.h"
 
 #define F4 ((u64)sizeof(f32))
-#define DEC_ATT_WAVES 8u   /* waves per decode-attention workgroup (as in decode_fused.hip) */
+#define DEC_QA_SEQ 2u      /* sequences per QKV + attention workgroup (as in decode_fused.hip) */
+#define DEC_QA_WPS 4u      /* waves per sequence there */
 #define DEC_HEAD_WAVES 8u  /* waves per LM-head workgroup (as in decode_fused.hip) */
 #define DEC_HEAD_KMAX 512u /* d_model bound of the LM-head kernel's LDS rows */
 
@@ -309,7 +310,8 @@ static void step_body(TrlmDecoder* d) {
         p.scale = d->scale;
         {
             void* args[] = { &p };
-            hip_launch(d->k_qkv_attn, (u32)Bc * d->H, 1, 1, 64 * DEC_ATT_WAVES, 1, 1, 0, args);
+            hip_launch(d->k_qkv_attn, cdiv32(d->B, DEC_QA_SEQ) * d->H, 1, 1, 64 * DEC_QA_SEQ * DEC_QA_WPS, 1, 1, 0,
+                       args);
         }
         /* x2 = x + (att @ Wo + bo) */
         p = base;

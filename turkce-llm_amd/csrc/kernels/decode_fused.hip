@@ -424,53 +424,67 @@ __device__ __forceinline__ void dec_attn_range(const f32x4_t qv, const float* __
     o_out = o;
 }
 
-#define DEC_ATT_WAVES 8
-
 // ------------------------------------------------- QKV projection + attention
-// One workgroup of 8 waves per (sequence b, head h) computes the head's q, k
-// and v of the new token itself -- RMSNorm(x[b]) @ Wqkv[:, head columns] + b,
-// RoPE on q and k at the position -- appends k and v to the cache, and runs
-// the attention of q over the cached keys 0 .. pos-1 (each wave a
-// contiguous range, dec_attn_range) and the new key, merged in wave order
-// with the new key last.  This removes the step's separate QKV kernel and its boundary: every
-// input of a head's attention is the row x[b] and a 3*HD-column slice of
-// Wqkv (the workgroups of a head read the same slice from cache).
+// One workgroup per head h and pair of sequences (b0, b0 + 1), 4 waves per
+// sequence: it forms the head's q, k and v of each sequence's new token
+// itself -- RMSNorm(x[b]) @ Wqkv[:, head columns] + b, RoPE on q and k at the
+// position -- appends k and v to the cache, and runs the attention of q over
+// the cached keys 0 .. pos-1 (each wave of the sequence a contiguous range,
+// dec_attn_range) and the new key, merged in wave order with the new key
+// last.  This removes the step's separate QKV kernel and its boundary: the
+// inputs of a head's attention are the row x[b] and a 3*HD-column slice of
+// Wqkv, which the workgroup reads once for its two sequences (measured
+// against one sequence of 8 waves, four of 2 or 4 waves and two of 8 waves
+// per workgroup: two of 4 is the fastest step).
 //
-// Projection: wave w takes rows [w*rw, (w+1)*rw) of the slice; lane
+// Projection: the workgroup's 8 waves split the rows of the slice; lane
 // (sub, c4) reads W[k][seg*D + h*HD + 4c4 .. +3] of the three segments for
 // rows k = k0 + RPI*g + sub, so one wave instruction covers RPI whole rows of
-// a segment.  The normalisation is applied after the sum,
-// out = r * sum_k (x[k] w[k]) W[k][c] + bias, r = 1/sqrt(mean(x^2) + eps) in
-// f64 as in k_rmsnorm_fwd.  The per-row values x[k] w[k] reach the lanes by
-// lane shuffles, and the partial sums go through LDS to wave 0, which adds
+// a segment, and multiplies them into both sequences' sums.  The
+// normalisation is applied after the sum, out = r * sum_k (x[k] w[k])
+// W[k][c] + bias, r = 1/sqrt(mean(x^2) + eps) in f64 as in k_rmsnorm_fwd.
+// The per-row values x[k] w[k] reach the lanes by lane shuffles, and the
+// partial sums go through LDS to the first wave of each sequence, which adds
 // them in wave order.  The first pass of the cache stream is issued before
 // the projection (it does not depend on q), so it is in flight meanwhile.
-template <int HD, int WAVES = DEC_ATT_WAVES, int NIT = 4>
+template <int HD, int SEQ, int WPS, int NIT = 4>
 __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
-    constexpr int LPR = HD / 4, RPI = 64 / LPR, PASS = NIT * RPI;
+    constexpr int LPR = HD / 4, RPI = 64 / LPR;
+    constexpr int TW = SEQ * WPS;               // waves of the workgroup
     constexpr int GB = 4;                       // row groups per load batch of the projection
-    __shared__ f32x4_t red[WAVES][3][LPR];      // the waves' partial q | k | v sums
-    __shared__ f32x4_t hv[3][LPR];              // the head's q, new k, new v
-    __shared__ float wm[WAVES], wl[WAVES];
-    __shared__ f32x4_t wo[WAVES][LPR];
-    __shared__ float s_new;
+    __shared__ f32x4_t red[TW][SEQ][3][LPR];    // the waves' partial q | k | v sums
+    __shared__ f32x4_t hv[SEQ][3][LPR];         // each sequence's q, new k, new v
+    __shared__ float wm[TW], wl[TW];
+    __shared__ f32x4_t wo[TW][LPR];
+    __shared__ float s_new[SEQ];
     const int pos = *p.pos;                     // the new token's position = cached keys
     // consecutive workgroups take different heads, so the workgroups on one
     // XCD (every 8th) read only a few of the heads' Wqkv slices
-    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
+    const int pr = blockIdx.x / p.H, h = blockIdx.x - pr * p.H;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int sq = wave / WPS, wr = wave - sq * WPS;   // this wave's sequence and its rank there
     const int sub = lane / LPR, c4 = lane % LPR;
     const int D = p.D;
     const float c2 = p.scale * DEC_LOG2E_F;
+    // the workgroup's sequences (a missing last one recomputes the first's
+    // values and stores nothing)
+    int bs[SEQ];
+#pragma unroll
+    for (int s = 0; s < SEQ; s++) {
+        const int bb = pr * SEQ + s;
+        bs[s] = bb < p.M ? bb : pr * SEQ;
+    }
+    const int b = bs[sq];
+    const bool b_ok = pr * SEQ + sq < p.M;
 
     // this wave's cached keys and its first pass's loads (clamped to row 0,
     // which the prefill always wrote; rows past the wave's keys weigh 0)
     const int n = pos;
-    const int per = ((n + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;
-    const int j0 = wave * per;
+    const int per = ((n + WPS - 1) / WPS + RPI - 1) / RPI * RPI;
+    const int j0 = wr * per;
     int j1 = j0 + per;
     if (j1 > n) j1 = n;
-    const long long head_rows = (long long)bh * p.ctx;
+    const long long head_rows = ((long long)b * p.H + h) * p.ctx;
     const float* kb = p.kc + head_rows * HD + 4 * c4;
     const float* vb = p.vc + head_rows * HD + 4 * c4;
     f32x4_t kn[NIT], vn[NIT];
@@ -482,33 +496,43 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
         vn[it] = ld4_stream(vb + off);
     }
 
-    // ---- projection of x[b] onto the head's q | k | v columns
-    const float* xr = p.a_ids ? p.E + (long long)p.ids[b] * p.lda : p.A + (long long)b * p.lda;
-    const int rw = ((D + WAVES - 1) / WAVES + RPI - 1) / RPI * RPI;   // rows per wave (<= 64 for D <= 512)
+    // ---- projection of the rows x[b] onto the head's q | k | v columns:
+    // the workgroup's waves split the slice's rows, each for every sequence
+    const float* xr[SEQ];
+#pragma unroll
+    for (int s = 0; s < SEQ; s++)
+        xr[s] = p.a_ids ? p.E + (long long)p.ids[bs[s]] * p.lda : p.A + (long long)bs[s] * p.lda;
+    const int rw = ((D + TW - 1) / TW + RPI - 1) / RPI * RPI;   // rows per wave (<= 64 for D <= 512)
     const int k0 = wave * rw;
     int k1 = k0 + rw;
     if (k1 > D) k1 = D;
-    // lane i < rw holds x[k0 + i] * w[k0 + i]
-    float xw;
+    // lane i < rw holds x[b][k0 + i] * w[k0 + i] of each sequence
+    float xw[SEQ];
     {
         const int k = k0 + lane;
         const int ks = k < k1 ? k : 0;
-        const float xv = xr[ks], wv = p.norm_w[ks];
-        xw = (k < k1 && lane < rw) ? xv * wv : 0.f;
+        const float wn = p.norm_w[ks];
+#pragma unroll
+        for (int s = 0; s < SEQ; s++) {
+            const float xv = xr[s][ks];
+            xw[s] = (k < k1 && lane < rw) ? xv * wn : 0.f;
+        }
     }
-    // wave 0 also forms the row's sum of squares for r
+    // the first wave of each sequence also forms its row's sum of squares for r
     float ss = 0.f;
-    if (wave == 0) {
+    if (wr == 0) {
         for (int q4 = lane; q4 < D / 4; q4 += 64) {
-            const f32x4_t v = ld4(xr + 4 * q4);
+            const f32x4_t v = ld4(xr[sq] + 4 * q4);
             ss += v[0] * v[0] + v[1] * v[1] + v[2] * v[2] + v[3] * v[3];
         }
         ss = wave_sum(ss);
     }
     const float* wcol = p.W + h * HD + 4 * c4;   // q column quad; k at + D, v at + 2D
-    f32x4_t acc[3];
+    f32x4_t acc[SEQ][3];
 #pragma unroll
-    for (int s = 0; s < 3; s++) acc[s] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+    for (int s = 0; s < SEQ; s++)
+#pragma unroll
+        for (int g = 0; g < 3; g++) acc[s][g] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     for (int g0 = 0; g0 < rw; g0 += GB * RPI) {
         f32x4_t wv[GB][3];
 #pragma unroll
@@ -516,39 +540,46 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
             const int k = k0 + g0 + j * RPI + sub;
             const long long ks = k < k1 ? k : 0;
 #pragma unroll
-            for (int s = 0; s < 3; s++) wv[j][s] = ld4(wcol + ks * p.ldw + s * D);
+            for (int g = 0; g < 3; g++) wv[j][g] = ld4(wcol + ks * p.ldw + g * D);
         }
 #pragma unroll
         for (int j = 0; j < GB; j++) {
             const int i = g0 + j * RPI + sub;           // row offset inside the wave's range
-            const float xk = __shfl(xw, i < 64 ? i : 63, WAVE);
             const bool kv = i < rw && k0 + i < k1;
 #pragma unroll
-            for (int s = 0; s < 3; s++) acc[s] += (kv ? xk : 0.f) * wv[j][s];
+            for (int s = 0; s < SEQ; s++) {
+                const float xk = __shfl(xw[s], i < 64 ? i : 63, WAVE);
+#pragma unroll
+                for (int g = 0; g < 3; g++) acc[s][g] += (kv ? xk : 0.f) * wv[j][g];
+            }
         }
     }
     // rows of the wave -> one partial per column quad
 #pragma unroll
     for (int sh = LPR; sh < 64; sh <<= 1)
 #pragma unroll
-        for (int s = 0; s < 3; s++)
+        for (int s = 0; s < SEQ; s++)
 #pragma unroll
-            for (int e = 0; e < 4; e++) acc[s][e] += __shfl_xor(acc[s][e], sh, WAVE);
+            for (int g = 0; g < 3; g++)
+#pragma unroll
+                for (int e = 0; e < 4; e++) acc[s][g][e] += __shfl_xor(acc[s][g][e], sh, WAVE);
     if (sub == 0) {
 #pragma unroll
-        for (int s = 0; s < 3; s++) red[wave][s][c4] = acc[s];
+        for (int s = 0; s < SEQ; s++)
+#pragma unroll
+            for (int g = 0; g < 3; g++) red[wave][s][g][c4] = acc[s][g];
     }
     __syncthreads();
-    if (wave == 0 && lane < 3 * LPR) {
-        const int s = lane / LPR, cq = lane % LPR;
-        f32x4_t y = red[0][s][cq];
+    if (wr == 0 && lane < 3 * LPR) {
+        const int g = lane / LPR, cq = lane % LPR;
+        f32x4_t y = red[0][sq][g][cq];
 #pragma unroll
-        for (int w = 1; w < WAVES; w++) y += red[w][s][cq];
+        for (int w = 1; w < TW; w++) y += red[w][sq][g][cq];
         const float r = 1.0f / (float)sqrt((double)(ss / (float)D + p.eps));
-        const f32x4_t bv = ld4(p.bias + s * D + h * HD + 4 * cq);
+        const f32x4_t bv = ld4(p.bias + g * D + h * HD + 4 * cq);
 #pragma unroll
         for (int e = 0; e < 4; e++) y[e] = y[e] * r + bv[e];
-        if (s < 2) {
+        if (g < 2) {
             // RoPE on the pairs (4cq, 4cq+1) and (4cq+2, 4cq+3)
 #pragma unroll
             for (int i = 0; i < 2; i++) {
@@ -559,18 +590,18 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
                 y[2 * i + 1] = ye * sn + yo * cs;
             }
         }
-        hv[s][cq] = y;
-        if (s > 0) *(f32x4_t*)((s == 1 ? p.kc : p.vc) + (head_rows + pos) * HD + 4 * cq) = y;
+        hv[sq][g][cq] = y;
+        if (g > 0 && b_ok) *(f32x4_t*)((g == 1 ? p.kc : p.vc) + (head_rows + pos) * HD + 4 * cq) = y;
     }
     __syncthreads();
-    const f32x4_t qv = hv[0][c4];
-    if (wave == 0) {
+    const f32x4_t qv = hv[sq][0][c4];
+    if (wr == 0) {
         // the new key's score, formed as the cached keys' scores are
-        const f32x4_t kv = hv[1][c4];
+        const f32x4_t kv = hv[sq][1][c4];
         float d = kv[0] * qv[0] + kv[1] * qv[1] + kv[2] * qv[2] + kv[3] * qv[3];
 #pragma unroll
         for (int sh = 1; sh < LPR; sh <<= 1) d += __shfl_xor(d, sh, WAVE);
-        if (lane == 0) s_new = d * c2;
+        if (lane == 0) s_new[sq] = d * c2;
     }
 
     // ---- attention over the cached keys, merged with the new key
@@ -580,29 +611,34 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
     if (sub == 0) wo[wave][c4] = o;
     if (lane == 0) { wm[wave] = mx; wl[wave] = lrow; }
     __syncthreads();
-    if (threadIdx.x < LPR) {
-        const float sn = s_new;
+    if (wr == 0 && lane < LPR && b_ok) {
+        const int w0 = sq * WPS;
+        const float sn = s_new[sq];
         float M = sn;
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) M = fmaxf(M, wm[w]);
+        for (int w = 0; w < WPS; w++) M = fmaxf(M, wm[w0 + w]);
         float L = 0.f;
         f32x4_t a = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int w = 0; w < WAVES; w++) {
-            const float wt = wm[w] == -INFINITY ? 0.f : exp2f(wm[w] - M);   // waves without keys weigh 0
-            L += wt * wl[w];
-            a += wt * wo[w][threadIdx.x];
+        for (int w = 0; w < WPS; w++) {
+            const float wt = wm[w0 + w] == -INFINITY ? 0.f : exp2f(wm[w0 + w] - M);   // waves without keys weigh 0
+            L += wt * wl[w0 + w];
+            a += wt * wo[w0 + w][lane];
         }
         const float wt = exp2f(sn - M);
         L += wt;
-        a += wt * hv[2][threadIdx.x];
-        *(f32x4_t*)(p.C + (long long)b * p.ldc + h * HD + 4 * threadIdx.x) = a / L;
+        a += wt * hv[sq][2][lane];
+        *(f32x4_t*)(p.C + (long long)b * p.ldc + h * HD + 4 * lane) = a / L;
     }
 }
 
-#define DEC_QKV_ATTN_KERNEL(HD)                                                                               \
-    extern "C" __global__ void __launch_bounds__(64 * DEC_ATT_WAVES) k_dec_qkv_attn_hd##HD(DecGemmParams p) { \
-        dec_qkv_attn<HD>(p);                                                                                  \
+// DEC_QA_SEQ sequences per workgroup, DEC_QA_WPS waves each
+#define DEC_QA_SEQ 2
+#define DEC_QA_WPS 4
+#define DEC_QKV_ATTN_KERNEL(HD)                                                                         \
+    extern "C" __global__ void __launch_bounds__(64 * DEC_QA_SEQ * DEC_QA_WPS)                           \
+        __attribute__((amdgpu_waves_per_eu(4))) k_dec_qkv_attn_hd##HD(DecGemmParams p) {               \
+        dec_qkv_attn<HD, DEC_QA_SEQ, DEC_QA_WPS>(p);                                                    \
     }
 DEC_QKV_ATTN_KERNEL(16)
 DEC_QKV_ATTN_KERNEL(32)
