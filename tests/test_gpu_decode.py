@@ -39,6 +39,8 @@ def last_rows(orc, model, params, ctx, B):
     (83, 128, 2, 2, 160, 2, 7, 4),     # head_dim 64
     (71, 128, 2, 1, 64, 2, 250, 12),   # keys cross the 256-key chunk boundary
     (53, 32, 2, 1, 32, 65, 3, 2),      # batch 65
+    (59, 96, 6, 2, 64, 3, 6, 4),       # six heads, odd batch: a workgroup with one sequence
+    (61, 192, 12, 2, 96, 3, 5, 4),     # twelve heads of 16
 ])
 def test_decode_equals_full_recompute(trlm, orc, V, D, H, L, F, B, P, S):
     model = orc.Model(V, D, H, L, F)
