@@ -53,13 +53,24 @@ __device__ __forceinline__ void rope4(const GemmParams& p, int row, int n, f32x4
     v[3] = a[2] * s1 + a[3] * c1;
 }
 
-__device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn) {
+__device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn, int& split) {
     const int num = p.tiles_m * p.tiles_n;
-    int bid = blockIdx.x;
-    // XCD-aware remap: hardware hands workgroup i to XCD (i % 8).
-    const int per = num >> 3;
+    // XCD-aware remap: hardware hands workgroup i to XCD (i % 8).  A split-K
+    // launch (a single GEMM, blockIdx.z = split) is remapped over all its
+    // workgroups in split-major order, so each XCD takes whole splits: the
+    // tiles of one split share its k-range of both operands, which then stays
+    // in that XCD's L2 instead of being fetched by every XCD.
+    const int splits = p.splits > 1 ? p.splits : 1;
+    const int all = num * splits;
+    int bid = blockIdx.x + (splits > 1 ? (int)blockIdx.z * num : 0);
+    const int per = all >> 3;
     int tile = bid;
     if (bid < (per << 3)) tile = (bid & 7) * per + (bid >> 3);
+    split = 0;
+    if (splits > 1) {
+        split = tile / num;
+        tile -= split * num;
+    }
     // Group 8 M-tiles so tiles that run together share A and B panels.
     const int GROUP = 8;
     int group_size = GROUP * p.tiles_n;
@@ -662,10 +673,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     constexpr int ASZ = TileLds<BM, BK, AK>::SIZE, BSZ = TileLds<BN, BK, BK_>::SIZE;
     __shared__ __attribute__((aligned(16))) float lds[2 * (ASZ + BSZ)];
 
-    int tm, tn;
-    gemm_tile_coords(p, tm, tn);
-    const int z = blockIdx.z;
-    const int batch = z / p.splits, split = z - batch * p.splits;
+    int tm, tn, split;
+    gemm_tile_coords(p, tm, tn, split);
+    const int batch = p.splits > 1 ? 0 : (int)blockIdx.z;   // split-K launches are single GEMMs
     const float* A = p.A + batch * p.sA;
     const float* B = p.B + batch * p.sB;
     float* C = p.C + batch * p.sC + split * p.sW;
