@@ -28,7 +28,6 @@ static u32 pidx(u32 layer, u32 k) { return trlm_pidx(layer, k); }
 static hipDeviceptr_t dptr(hipDeviceptr_t base, u64 floats) { return (hipDeviceptr_t)((char*)base + floats * F4); }
 static hipDeviceptr_t P_(const GpuTrainer* g, u32 i) { return dptr(g->params, g->offsets[i]); }
 static hipDeviceptr_t G_(const GpuTrainer* g, u32 i) { return dptr(g->grads, g->offsets[i]); }
-static hipDeviceptr_t dalloc(u64 floats) { return hip_alloc(floats * F4); }
 
 static void fatal(const char* msg) {
     fprintf(stderr, "[HIP ERROR] gpu_train: %s\n", msg);
@@ -145,16 +144,106 @@ static AttnParams attn_params(GpuTrainer* g) {
 
 /* ---------------- create / destroy ---------------- */
 
+/* Every device buffer of a trainer lives in one allocation, carved into
+ * 256-byte aligned slices: the buffer plan below lists (slot, floats) pairs,
+ * carve() sizes and places them all, then assigns the slots. */
+#define CARVE_ALIGN 256u
+#define GPU_TRAIN_PLAN_MAX (4u + 11u * LM_MAX_LAYERS + 64u)   /* flat buffers, layer activations, the rest */
+typedef struct CarvePlan {
+    hipDeviceptr_t* slot[GPU_TRAIN_PLAN_MAX];
+    u64 bytes[GPU_TRAIN_PLAN_MAX];
+    u32 n;
+} CarvePlan;
+
+static void want(CarvePlan* cp, hipDeviceptr_t* slot, u64 bytes) {
+    if (cp->n == GPU_TRAIN_PLAN_MAX) fatal("too many trainer buffers");
+    cp->slot[cp->n] = slot;
+    cp->bytes[cp->n] = bytes;
+    cp->n++;
+}
+
+static void want_f(CarvePlan* cp, hipDeviceptr_t* slot, u64 floats) { want(cp, slot, floats * F4); }
+
+static void carve(CarvePlan* cp) {
+    u64 total = 0;
+    for (u32 i = 0; i < cp->n; i++) total += (cp->bytes[i] + CARVE_ALIGN - 1) / CARVE_ALIGN * CARVE_ALIGN;
+    char* base = (char*)hip_alloc(total);
+    for (u32 i = 0; i < cp->n; i++) {
+        *cp->slot[i] = (hipDeviceptr_t)base;
+        base += (cp->bytes[i] + CARVE_ALIGN - 1) / CARVE_ALIGN * CARVE_ALIGN;
+    }
+}
+
+/* The buffers of a B x T trainer (sizes in floats unless noted). */
+static void plan_buffers(GpuTrainer* g, CarvePlan* cp) {
+    const u64 N = g->N, D = g->D, F = g->F, BHT = (u64)g->B * g->H * g->T;
+    const u64 nqb = ((u64)g->T + 63) / 64, part_rows = part_buffer_rows(N);
+    /* the flat parameter-sized buffers, lm_collect_params order */
+    hipDeviceptr_t* flat[4] = { &g->params, &g->grads, &g->adam_m, &g->adam_v };
+    for (u32 i = 0; i < 4; i++) want_f(cp, flat[i], g->total_scalars);
+    /* what each layer keeps from its forward for the backward */
+    for (u32 l = 0; l < g->L; l++) {
+        GpuLayerActs* a = &g->layers[l];
+        const struct { hipDeviceptr_t* p; u64 n; } acts[] = {
+            { &a->x_in, N * D }, { &a->n1, N * D }, { &a->r1, N },     { &a->qkv, N * 3 * D },
+            { &a->att, N * D },  { &a->lse, BHT },  { &a->x2, N * D }, { &a->n2, N * D },
+            { &a->r2, N },       { &a->gu, N * 2 * F }, { &a->h, N * F },
+        };
+        for (u32 i = 0; i < sizeof(acts) / sizeof(acts[0]); i++) want_f(cp, acts[i].p, acts[i].n);
+    }
+    /* head and loss */
+    want_f(cp, &g->x_final, N * D);
+    want_f(cp, &g->nf, N * D);
+    want_f(cp, &g->rf, N);
+    want_f(cp, &g->logits, N * (u64)g->ldv);
+    want_f(cp, &g->ce_stats, N * (u64)g->ce_stats_cap * 2);
+    want_f(cp, &g->ce_zt, N);
+    want_f(cp, &g->loss_rows, N);
+    want_f(cp, &g->norm_partial, GPU_TRAIN_NORM_BLOCKS);
+    /* backward scratch: the residual-gradient ring, the by-parity pairs the
+     * side stream reads, the causal dS blocks of one layer, norm partials */
+    for (u32 i = 0; i < GPU_TRAIN_DRES_RING; i++) want_f(cp, &g->dres[i], N * D);
+    for (u32 i = 0; i < 2; i++) {
+        want_f(cp, &g->dqkv[i], N * 3 * D);
+        want_f(cp, &g->dgu[i], N * 2 * F);
+        want_f(cp, &g->part[i][0], part_rows * D);
+        want_f(cp, &g->part[i][1], part_rows * D);
+    }
+    want_f(cp, &g->part_final, part_rows * D);
+    want_f(cp, &g->dn, N * D);
+    want_f(cp, &g->datt, N * D);
+    want_f(cp, &g->dh, N * F);
+    want_f(cp, &g->dvec, BHT);
+    want_f(cp, &g->att_ds, (u64)g->B * g->H * (nqb * (nqb + 1) / 2) * 4096);
+    /* token ids and the embedding backward's row groups (u32) */
+    want(cp, &g->ids, N * sizeof(u32));
+    want(cp, &g->targets, N * sizeof(u32));
+    want(cp, &g->emb_order, N * sizeof(u32));
+    want(cp, &g->emb_seg, (2 * N + 1) * sizeof(u32));
+    /* RoPE tables [T][hd/2] */
+    want_f(cp, &g->cos_t, (u64)g->T * (g->hd / 2));
+    want_f(cp, &g->sin_t, (u64)g->T * (g->hd / 2));
+}
+
 GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,
                               Node** params, u32 num_params, u32 batch_size, u32 seq_len) {
     GpuTrainer g;
     memset(&g, 0, sizeof(g));
-    g.V = model->vocab_size; g.D = model->d_model; g.H = model->num_heads; g.L = model->num_layers;
+    /* model and batch geometry; F is the feed-forward width, read off the
+     * first block's down projection [F, D] */
+    const u32 d_model = model->d_model, heads = model->num_heads;
+    g.V = model->vocab_size;
+    g.L = model->num_layers;
+    g.D = d_model;
+    g.H = heads;
+    g.hd = heads ? d_model / heads : 0;
     g.F = (u32)model->blocks[0].ffn.w_down->value.shape[0];
-    g.T = seq_len; g.B = batch_size; g.N = batch_size * seq_len;
-    g.hd = g.D / g.H;
     g.eps = model->eps;
+    g.B = batch_size;
+    g.T = seq_len;
+    g.N = batch_size * seq_len;
     g.ldv = (g.V + 3u) & ~3u;
+    g.ce_stats_cap = 2 * (i32)((g.V + 63) / 64);     /* two entries per 64-wide (smallest) tile column */
     if (g.L > LM_MAX_LAYERS || num_params != 10u * g.L + 2u) fatal("parameter list does not match the model");
     if (g.D % g.H != 0 || g.D % 4 != 0) fatal("d_model must be a multiple of 4 and of num_heads");
     if (g.hd != 16 && g.hd != 32 && g.hd != 64) fatal("head_dim must be 16, 32 or 64");
@@ -163,81 +252,35 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     hip_set_current(&g.hip);
     g.gemm = NULL;   /* created below, after g.hip has its final address in the caller */
 
+    /* flat layout: tensor i at offsets[i] of every parameter-sized buffer */
     g.num_params = num_params;
-    u64 off = 0;
+    g.total_scalars = 0;
     for (u32 i = 0; i < num_params; i++) {
-        g.offsets[i] = off;
         g.numels[i] = params[i]->value.numel;
-        off += params[i]->value.numel;
+        g.offsets[i] = g.total_scalars;
+        g.total_scalars += g.numels[i];
     }
-    g.total_scalars = off;
-    g.params = dalloc(off);
-    g.grads = dalloc(off);
-    g.adam_m = dalloc(off);
-    g.adam_v = dalloc(off);
-    hip_memset_zero(g.adam_m, off * F4);
-    hip_memset_zero(g.adam_v, off * F4);
-    hip_memset_zero(g.grads, off * F4);
+    CarvePlan* cp = (CarvePlan*)calloc(1, sizeof(CarvePlan));
+    if (!cp) fatal("out of host memory");
+    plan_buffers(&g, cp);
+    carve(cp);
+    free(cp);
+    hip_memset_zero(g.grads, g.total_scalars * F4);
+    hip_memset_zero(g.adam_m, g.total_scalars * F4);
+    hip_memset_zero(g.adam_v, g.total_scalars * F4);
+    hip_memset_zero(g.logits, (u64)g.N * g.ldv * F4);
 
-    u64 N = g.N, D = g.D, F = g.F, BHT = (u64)g.B * g.H * g.T;
-    for (u32 l = 0; l < g.L; l++) {
-        GpuLayerActs* a = &g.layers[l];
-        a->x_in = dalloc(N * D);
-        a->n1 = dalloc(N * D);
-        a->r1 = dalloc(N);
-        a->qkv = dalloc(N * 3 * D);
-        a->att = dalloc(N * D);
-        a->lse = dalloc(BHT);
-        a->x2 = dalloc(N * D);
-        a->n2 = dalloc(N * D);
-        a->r2 = dalloc(N);
-        a->gu = dalloc(N * 2 * F);
-        a->h = dalloc(N * F);
-    }
-    g.x_final = dalloc(N * D);
-    g.nf = dalloc(N * D);
-    g.rf = dalloc(N);
-    g.logits = dalloc(N * (u64)g.ldv);
-    hip_memset_zero(g.logits, N * (u64)g.ldv * F4);
-    g.ce_stats_cap = 2 * (i32)((g.V + 63) / 64);     /* two entries per 64-wide (smallest) tile column */
-    g.ce_stats = dalloc(N * (u64)g.ce_stats_cap * 2);
-    g.ce_zt = dalloc(N);
-
-    for (u32 i = 0; i < GPU_TRAIN_DRES_RING; i++) g.dres[i] = dalloc(N * D);
-    g.dn = dalloc(N * D);
-    g.datt = dalloc(N * D);
-    g.dh = dalloc(N * F);
-    for (u32 i = 0; i < 2; i++) {
-        g.dqkv[i] = dalloc(N * 3 * D);
-        g.dgu[i] = dalloc(N * 2 * F);
-    }
-    g.dvec = dalloc(BHT);
-    {
-        u64 nqb = ((u64)g.T + 63) / 64;
-        g.att_ds = dalloc((u64)g.B * g.H * (nqb * (nqb + 1) / 2) * 4096);
-    }
-    u64 part_rows = part_buffer_rows(N);   /* RMSNorm weight-gradient partials + their group sums */
-    for (u32 i = 0; i < 4; i++) g.part[i / 2][i % 2] = dalloc(part_rows * D);
-    g.part_final = dalloc(part_rows * D);
-
-    g.ids = hip_alloc(N * sizeof(u32));
-    g.targets = hip_alloc(N * sizeof(u32));
-    g.loss_rows = dalloc(N);
-    g.emb_order = hip_alloc(N * sizeof(u32));
-    g.emb_seg = hip_alloc((2 * N + 1) * sizeof(u32));
+    const u64 N = g.N;
     g.host_loss_rows = (f32*)allocator_alloc(alloc, N * F4);
     g.host_emb = (u32*)allocator_alloc(alloc, (3 * N + 1 + (u64)g.V + 1) * sizeof(u32));
-    g.norm_partial = dalloc(GPU_TRAIN_NORM_BLOCKS);
     g.host_norm_partial = (f32*)allocator_alloc(alloc, GPU_TRAIN_NORM_BLOCKS * F4);
 
     /* RoPE tables, built on the host exactly as the CPU path builds them
      * (gpu_train.c:239-247, model/rope.c) */
-    u64 cshape[2] = { g.T, g.hd / 2 };
+    u64 cshape[2] = { g.T, g.hd / 2 };   /* the slots planned above */
     Tensor cos_t = tensor_create(alloc, cshape, 2);
     Tensor sin_t = tensor_create(alloc, cshape, 2);
     rope_build_tables(&cos_t, &sin_t, g.T, g.hd, 10000.0f);
-    g.cos_t = dalloc(cos_t.numel);
-    g.sin_t = dalloc(sin_t.numel);
     hip_h2d(g.cos_t, cos_t.data, cos_t.numel * F4);
     hip_h2d(g.sin_t, sin_t.data, sin_t.numel * F4);
 
@@ -300,40 +343,66 @@ void gpu_trainer_destroy(GpuTrainer* g) {
 
 /* ---------------- CPU mirror <-> GPU (gpu_train.c:258-294) ---------------- */
 
-void gpu_trainer_upload(GpuTrainer* g, Node** params, const AdamOptimizer* opt) {
-    hip_set_current(&g->hip);
+/* Copies between one flat device buffer and the caller's per-tensor host
+ * arrays (host[i]: tensor i, numels[i] floats at offsets[i] of the buffer),
+ * synchronously.  Tensors that lie back to back in host memory -- the
+ * runtime's arena places a model's parameters that way -- travel as one
+ * transfer. */
+static void mirror(GpuTrainer* g, hipDeviceptr_t flat, f32* const* host, int to_device) {
+    u32 i = 0;
+    while (i < g->num_params) {
+        u64 run = g->numels[i];
+        u32 j = i + 1;
+        while (j < g->num_params && host[j] == host[i] + run) run += g->numels[j++];
+        hipDeviceptr_t dev = dptr(flat, g->offsets[i]);
+        if (to_device) hip_h2d(dev, host[i], run * F4);
+        else hip_d2h(host[i], dev, run * F4);
+        i = j;
+    }
+}
+
+enum { HOST_VALUE, HOST_GRAD, HOST_ADAM_M, HOST_ADAM_V };
+
+/* The host arrays of one kind for every tensor. */
+static void host_arrays(const GpuTrainer* g, Node** params, const AdamOptimizer* opt, int kind, f32** out) {
     for (u32 i = 0; i < g->num_params; i++) {
-        hip_h2d(P_(g, i), params[i]->value.data, g->numels[i] * F4);
-        if (opt != NULL_PTR) {
-            hip_h2d(dptr(g->adam_m, g->offsets[i]), opt->m[i].data, g->numels[i] * F4);
-            hip_h2d(dptr(g->adam_v, g->offsets[i]), opt->v[i].data, g->numels[i] * F4);
+        switch (kind) {
+            case HOST_VALUE: out[i] = params[i]->value.data; break;
+            case HOST_GRAD: out[i] = params[i]->grad.data; break;
+            case HOST_ADAM_M: out[i] = opt->m[i].data; break;
+            default: out[i] = opt->v[i].data; break;
         }
+    }
+}
+
+static void mirror_kind(GpuTrainer* g, Node** params, const AdamOptimizer* opt, int kind, int to_device) {
+    f32* host[GPU_TRAIN_MAX_PARAMS];
+    const hipDeviceptr_t flat[4] = { g->params, g->grads, g->adam_m, g->adam_v };
+    hip_set_current(&g->hip);
+    host_arrays(g, params, opt, kind, host);
+    mirror(g, flat[kind], host, to_device);
+}
+
+void gpu_trainer_upload(GpuTrainer* g, Node** params, const AdamOptimizer* opt) {
+    mirror_kind(g, params, opt, HOST_VALUE, 1);
+    if (opt != NULL_PTR) {
+        mirror_kind(g, params, opt, HOST_ADAM_M, 1);
+        mirror_kind(g, params, opt, HOST_ADAM_V, 1);
     }
 }
 
 void gpu_trainer_download(GpuTrainer* g, Node** params, AdamOptimizer* opt) {
-    hip_set_current(&g->hip);
-    for (u32 i = 0; i < g->num_params; i++) {
-        hip_d2h(params[i]->value.data, P_(g, i), g->numels[i] * F4);
-        if (opt != NULL_PTR) {
-            hip_d2h(opt->m[i].data, dptr(g->adam_m, g->offsets[i]), g->numels[i] * F4);
-            hip_d2h(opt->v[i].data, dptr(g->adam_v, g->offsets[i]), g->numels[i] * F4);
-        }
+    mirror_kind(g, params, opt, HOST_VALUE, 0);
+    if (opt != NULL_PTR) {
+        mirror_kind(g, params, opt, HOST_ADAM_M, 0);
+        mirror_kind(g, params, opt, HOST_ADAM_V, 0);
     }
 }
 
-void gpu_trainer_download_grads(GpuTrainer* g, Node** params) {
-    hip_set_current(&g->hip);
-    for (u32 i = 0; i < g->num_params; i++) hip_d2h(params[i]->grad.data, G_(g, i), g->numels[i] * F4);
-}
+void gpu_trainer_download_grads(GpuTrainer* g, Node** params) { mirror_kind(g, params, NULL_PTR, HOST_GRAD, 0); }
 
-void gpu_trainer_upload_grads(GpuTrainer* g, Node** params) {
-    hip_set_current(&g->hip);
-    for (u32 i = 0; i < g->num_params; i++) hip_h2d(G_(g, i), params[i]->grad.data, g->numels[i] * F4);
-}
+void gpu_trainer_upload_grads(GpuTrainer* g, Node** params) { mirror_kind(g, params, NULL_PTR, HOST_GRAD, 1); }
 
-/* Window of sequence w: pcg_seed(seed_base*1000003 + w, 99 + w), start
- * uniform in [0, num_tokens - T - 1)  (gpu_train.c:296-307). */
 void gpu_trainer_sample_batch(const u32* tokens, u64 num_tokens, u32 seq_len, u32 batch_size,
                               u64 seed_base, u32* ids_out, u32* targets_out) {
     i64 max_start = (i64)(num_tokens - seq_len - 1);
