@@ -18,6 +18,10 @@ returns 1 on any).
   tests/test_gpu_ops.c      node_matmul2d_gpu forward/backward vs the CPU
   tests/test_lm_model_gpu.c lm_forward with GPU layers vs the CPU
   tests/test_batched_lm.c   batched lm_forward on the GPU path
+  tests/test_data_parallel.c data_parallel_step with 8 worker threads on
+                            the gpu_ops worker slots vs one thread
+  tests/test_resume.c       training resumed from a checkpoint with the
+                            gpu_ops worker slots equals the uninterrupted run
 """
 import os
 import subprocess
@@ -29,7 +33,8 @@ pytestmark = pytest.mark.gpu
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 BIN = os.path.join(ROOT, "oracle", "_ref", "dropin")
-PROGRAMS = ["tests_test_gpu_ops", "tests_test_lm_model_gpu", "tests_test_batched_lm", "tests_test_gpu_train"]
+PROGRAMS = ["tests_test_gpu_ops", "tests_test_lm_model_gpu", "tests_test_batched_lm", "tests_test_gpu_train",
+            "tests_test_data_parallel", "tests_test_resume"]
 
 
 @pytest.mark.parametrize("prog", PROGRAMS)
