@@ -13,7 +13,7 @@
 //   k_dec_out   x2 = x + (att @ Wo + bo)
 //   k_dec_gu    h = SwiGLU(RMSNorm(x2) @ Wgu + bgu)
 //   k_dec_down  x = x2 + (h @ Wd + bd)
-//   k_dec_head  logits = RMSNorm(x) @ E^T, then the position moves on
+//   k_dec_head_k*  logits = RMSNorm(x) @ E^T, then the position moves on
 //
 // GEMM tiling.  The output is cut into 16 x 16 blocks, one per workgroup
 // (two for the gate/up pair), so even a 64-row product spreads over
