@@ -5,11 +5,11 @@
 // latency and HBM, not by the matrix cores.  The reference computes it as
 // the full-window lm_forward (training/generate.c:186-212); within the
 // context the last row needs only the cached keys and values, so a step is:
-//   k_dec_qkv_attn  per (sequence, head): RMSNorm(x) @ Wqkv + b for the
-//               head's columns, RoPE on q and k at the position, k and v
-//               appended to the cache, then q over the cached keys and the
-//               new one, the 8 waves splitting the context, merged in wave
-//               order                                  (layer 0: x = E[ids])
+//   k_dec_qkv_attn  per head and pair of sequences: RMSNorm(x) @ Wqkv + b
+//               for the head's columns, RoPE on q and k at the position, k
+//               and v appended to the cache, then q over the cached keys and
+//               the new one, 4 waves per sequence splitting the context,
+//               merged in wave order                   (layer 0: x = E[ids])
 //   k_dec_out   x2 = x + (att @ Wo + bo)
 //   k_dec_gu    h = SwiGLU(RMSNorm(x2) @ Wgu + bgu)
 //   k_dec_down  x = x2 + (h @ Wd + bd)
