@@ -196,23 +196,44 @@ __device__ __forceinline__ void att_store_rows(float* rowp, const f32x16* acc, i
         }
 }
 
+// Causal work per query block grows with its index, so the workgroup ->
+// (head, query block) map ranks the jobs longest first (rank r: query block
+// nqb-1 - r/BH, head r%BH, BH = gridDim.x heads) and lets dispatch round k
+// (256 workgroups, one per CU, consecutive workgroups going to different
+// CUs) take its ranks in reverse order when k is odd: a CU then holds a long,
+// a short and a middle block (per-CU key blocks 23..28 instead of 18..33 for
+// 768 workgroups of 16 blocks).
+__device__ __forceinline__ void att_snake_job(int nqb, int& qb, int& bh) {
+    const int BH = gridDim.x, total = BH * gridDim.y;
+    const int L = blockIdx.y * BH + blockIdx.x, r = L / 256, lo = r * 256;
+    const int m = (total - lo) < 256 ? (total - lo) : 256;
+    const int rank = (r & 1) ? lo + (m - 1) - (L - lo) : L;
+    qb = nqb - 1 - rank / BH;
+    bh = rank - (rank / BH) * BH;
+}
+
 // =========================================================== forward
-// grid (B*H, ceil(T/64)), 256 threads.  Wave w: query group g = w&1 (32
-// queries), key partition part = w>>1 (key blocks part, part+2, ...).
+// grid (B*H, ceil(T/64)), 256 threads, three workgroups per CU.  Wave w:
+// query group g = w&1 (32 queries), key half part = w>>1: every stage loads
+// one 64-key block (K and V^T in LDS, the next block fetched into registers
+// meanwhile) and part p takes its keys 32p .. 32p+31; each wave keeps its own
+// online softmax, and the two parts are merged at the end.  One K and one V^T
+// tile per stage (35 KB of LDS) and 167 registers let three workgroups share
+// a CU, so all 768 workgroups of B8 T1024 are resident at once and the
+// snake order (att_snake_job) evens out the causal work per CU.
 template <int HD>
 __device__ void flash_fwd(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
     constexpr int LD = HD + 4;
     constexpr int KS = 64 * LD, VS = HD * ATT_LDT;                     // K [64][LD], V^T [HD][ATT_LDT]
-    __shared__ __attribute__((aligned(16))) float lds[2 * (KS + VS)];  // [part][K | V^T]
+    __shared__ __attribute__((aligned(16))) float lds[KS + VS];        // K | V^T of the stage's key block
 
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
     const int grp = wave & 1, part = wave >> 1;
     const int nqb = (p.T + 63) / 64;
-    // blockIdx.x (dispatched fastest) runs over heads, so every head's
-    // longest (latest) query block is dispatched before any shorter one
-    const int qb = nqb - 1 - (int)blockIdx.y;
-    const int bh = blockIdx.x, b = bh / p.H, h = bh - b * p.H;
+    int qb, bh;
+    att_snake_job(nqb, qb, bh);
+    const int b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
     const float* qkv = p.qkv + rowbase * p.ldq;
     const int qcol = h * HD, kcol = p.D + h * HD, vcol = 2 * p.D + h * HD;
@@ -232,118 +253,86 @@ __device__ void flash_fwd(const AttnParams& p) {
     int kv_end = (qb + 1) * 64;
     if (kv_end > p.T) kv_end = p.T;
     const int nkv = (kv_end + 63) / 64;
-    const int niter = (nkv + 1) / 2;
-    const float* Ks = lds + part * (KS + VS);
-    const float* Vt = Ks + KS;
-    // K and V of the stage's two key blocks go through registers, fetched one
-    // stage ahead so that their loads overlap the previous stage's MFMAs.
-    // Loads and stores are unconditional (blocks past the end load clamped
-    // rows and store zeros that no wave reads), so the compiler's wait
-    // tracking sees one straight path and never waits for a fetch early.
-    AttTile<HD> tk[2];
-    AttTileT<HD> tv[2];
-    auto fetch = [&](int it) {
-#pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            const int kb = 2 * it + pp;
-            tk[pp].load(qkv, p.ldq, kb * 64, p.T, kcol);
-            tv[pp].load(qkv, p.ldq, kb * 64, p.T, vcol);
-        }
+    const float* Ks = lds;
+    const float* Vt = lds + KS;
+    // one key block per stage: part p of the wave pair takes its keys
+    // 32p .. 32p+31; K and V^T of the next block are fetched one stage ahead
+    AttTile<HD> tk;
+    AttTileT<HD> tv;
+    auto fetch = [&](int kb) {
+        tk.load(qkv, p.ldq, kb * 64, p.T, kcol);
+        tv.load(qkv, p.ldq, kb * 64, p.T, vcol);
     };
     fetch(0);
     att_settle<HD / 8>(qf);
-    for (int it = 0; it < niter; it++) {
+    for (int kb = 0; kb < nkv; kb++) {
         __syncthreads();
-#pragma unroll
-        for (int pp = 0; pp < 2; pp++) {
-            tk[pp].store(lds + pp * (KS + VS), (2 * it + pp) * 64, kv_end);
-            tv[pp].store(lds + pp * (KS + VS) + KS, (2 * it + pp) * 64, kv_end);
-        }
+        tk.store(lds, kb * 64, kv_end);
+        tv.store(lds + KS, kb * 64, kv_end);
         __syncthreads();
-        fetch(it + 1);
-        const int kb = 2 * it + part;
-        const int kv0 = kb * 64;
-        if (kb >= nkv || kv0 > qw0 + 31) continue;
+        fetch(kb + 1);
+        const int kv0 = kb * 64 + part * 32;
+        if (kv0 > qw0 + 31) continue;
 
-        f32x16 s[2];
+        f32x16 s;
 #pragma unroll
-        for (int c = 0; c < 2; c++) {
+        for (int r = 0; r < 16; r++) s[r] = 0.f;
 #pragma unroll
-            for (int r = 0; r < 16; r++) s[c][r] = 0.f;
+        for (int j = 0; j < HD / 8; j++) {
+            f32x4 kf = att_frag<HD>(Ks, part * 32, j, lane);
 #pragma unroll
-            for (int j = 0; j < HD / 8; j++) {
-                f32x4 kf = att_frag<HD>(Ks, c * 32, j, lane);
-#pragma unroll
-                for (int t = 0; t < 4; t++) s[c] = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[j][t], s[c], 0, 0, 0);
-            }
+            for (int t = 0; t < 4; t++) s = __builtin_amdgcn_mfma_f32_32x32x2f32(kf[t], qf[j][t], s, 0, 0, 0);
         }
-        // one K-fragment read between consecutive groups of 4 MFMAs
 #pragma unroll
-        for (int q = 0; q < HD / 4; q++) {
+        for (int q = 0; q < HD / 8; q++) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
-        // Causal mask on the diagonal block only (the block index is
-        // wave-uniform); the max is taken on the raw scores (the scale is
-        // positive) and the scale folds into the exponent's FMA.  Every
-        // processed block holds key kv0 <= qpos, so each row has a finite max.
-        if (kv0 + 63 > qw0) {
+        if (kv0 + 31 > qw0) {
 #pragma unroll
-            for (int c = 0; c < 2; c++)
-#pragma unroll
-                for (int r = 0; r < 16; r++) {
-                    const int kpos = kv0 + c * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-                    if (kpos > qpos) s[c][r] = -INFINITY;
-                }
+            for (int r = 0; r < 16; r++) {
+                const int kpos = kv0 + 8 * (r >> 2) + 4 * half + (r & 3);
+                if (kpos > qpos) s[r] = -INFINITY;
+            }
         }
-        float mr = s[0][0];
+        float mr = s[0];
 #pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) mr = fmaxf(mr, s[c][r]);
+        for (int r = 0; r < 16; r++) mr = fmaxf(mr, s[r]);
         mr = fmaxf(mr, __shfl_xor(mr, 32, WAVE));
         const float mx = fmaxf(m, mr * c2);
         const float alpha = __builtin_amdgcn_exp2f(m - mx);
         m = mx;
         float ls = 0.f;
 #pragma unroll
-        for (int c = 0; c < 2; c++)
-#pragma unroll
-            for (int r = 0; r < 16; r++) {
-                float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[c][r], c2, -mx));
-                s[c][r] = e;
-                ls += e;
-            }
+        for (int r = 0; r < 16; r++) {
+            float e = __builtin_amdgcn_exp2f(__builtin_fmaf(s[r], c2, -mx));
+            s[r] = e;
+            ls += e;
+        }
         l = l * alpha + ls;
-        // rescale only when some row's max moved (alpha != 1)
         if (__ballot(alpha != 1.0f)) {
 #pragma unroll
             for (int d = 0; d < DB; d++)
 #pragma unroll
                 for (int r = 0; r < 16; r++) o[d][r] *= alpha;
         }
-        // O^T += V^T P^T: registers 4g..4g+3 of s[c] hold keys
-        // c*32 + 8g + 4*half + (0..3), one 128-bit read of V^T each
 #pragma unroll
-        for (int c = 0; c < 2; c++)
+        for (int g = 0; g < 4; g++) {
+            f32x4 vt[DB];
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                f32x4 vt[DB];
-#pragma unroll
-                for (int d = 0; d < DB; d++) {
-                    const int dc = d * 32 + (lane & 31);
-                    vt[d] = (dc < HD) ? *(const f32x4*)(Vt + dc * ATT_LDT + c * 32 + 8 * g + 4 * half)
-                                      : f32x4{0.f, 0.f, 0.f, 0.f};
-                }
-#pragma unroll
-                for (int t = 0; t < 4; t++)
-#pragma unroll
-                    for (int d = 0; d < DB; d++)
-                        o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[d][t], s[c][4 * g + t], o[d], 0, 0, 0);
+            for (int d = 0; d < DB; d++) {
+                const int dc = d * 32 + (lane & 31);
+                vt[d] = (dc < HD) ? *(const f32x4*)(Vt + dc * ATT_LDT + part * 32 + 8 * g + 4 * half)
+                                  : f32x4{0.f, 0.f, 0.f, 0.f};
             }
-        // one V^T-fragment read between consecutive groups of 4 MFMAs
 #pragma unroll
-        for (int q = 0; q < 8 * DB; q++) {
+            for (int t = 0; t < 4; t++)
+#pragma unroll
+                for (int d = 0; d < DB; d++)
+                    o[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(vt[d][t], s[4 * g + t], o[d], 0, 0, 0);
+        }
+#pragma unroll
+        for (int q = 0; q < 4 * DB; q++) {
             __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
             __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);
         }
@@ -377,6 +366,7 @@ __device__ void flash_fwd(const AttnParams& p) {
         }
     }
 }
+
 
 // =========================================================== backward dK, dV
 // grid (B*H, ceil(T/64)).  Wave w: key group g = w&1 (32 keys), query
@@ -662,7 +652,7 @@ __device__ void attn_dvec(const AttnParams& p) {
 }
 
 #define ATT_KERNELS(HD)                                                                                   \
-    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_fwd_hd##HD(AttnParams p) { \
+    extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(3))) k_attn_fwd_hd##HD(AttnParams p) { \
         flash_fwd<HD>(p);                                                                                 \
     }                                                                                                     \
     extern "C" __global__ void __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2))) k_attn_bwd_dkv_hd##HD(AttnParams p) { \
