@@ -3,7 +3,9 @@ assertions of the reference's tests/test_gpu_train.c, at a 1e-4 bar.
 
 Cases (test_gpu_train.c:261-271): small shapes off every tile grid
 (V50 D32 H2 L2 F48 T12 B5), long context (V500 D64 H2 L2 F128 T1024 B2),
-and the real model (V31769 D384 H6 L12 F1024 T128 B4).  Inputs exactly as
+and the real model (V31769 D384 H6 L12 F1024 T128 B4); plus ragged
+attention blocks and 320 attention workgroups (more than one dispatch
+round of 256).  Inputs exactly as
 the reference test builds them: weights lm_init(pcg_seed(1337,1)), tokens
 pcg_range_i64(0, V-1) from pcg_seed(4242,7), batch seed 2026.
 
@@ -28,6 +30,9 @@ CASES = {
     "real_scale": dict(V=31769, D=384, H=6, L=12, F=1024, T=128, B=4, ntok=200000),
     # several 64-row attention blocks with a ragged last one (hd 16)
     "ragged_blocks": dict(V=300, D=64, H=4, L=2, F=96, T=200, B=3, ntok=8000),
+    # 320 attention workgroups (B*H*blocks): the attention forward's order
+    # reverses its second dispatch round of 256, here a partial one (hd 64)
+    "many_blocks": dict(V=200, D=128, H=2, L=1, F=96, T=640, B=16, ntok=20000),
 }
 TOL = 1e-4
 
