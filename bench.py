@@ -697,7 +697,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one MI355X: every box in this build has one GPU, and the multi-GPU design "
-              "(RCCL data parallel) is not implemented (see DESIGN.md). Run with --gpus 1.", file=sys.stderr)
+              "(RCCL data parallel over the gpu_ops worker slots) is not implemented. Run with --gpus 1.", file=sys.stderr)
         sys.exit(2)
 
     trlm = load_trlm()

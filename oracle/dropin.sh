@@ -2,8 +2,8 @@
 # dropin.sh -- TEST INFRASTRUCTURE ONLY: the drop-in binding, built for real.
 #
 # Builds every program of the reference (scripts/build_all.sh:24-40 compiles
-# each main against all non-main objects) the way INTEGRATION.md's binding
-# describes, from the reference's sources where they lie:
+# each main against all non-main objects) the way a maintainer binds this
+# library to the reference, from the reference's sources where they lie:
 #   - an overlay of the reference tree (real directories, a symlink per file,
 #     in a temporary directory outside this repository) in which
 #     model/gpu_train.h and model/gpu_ops.h are this build's headers and

@@ -313,7 +313,7 @@ def test_reference_programs_link_against_the_library(trlm):
     """oracle/dropin.sh: the reference's own programs, compiled against
     include/ as model/gpu_train.h, model/gpu_ops.h (+ hip_backend.h,
     trlm_host.h, trlm_ext.h), link with libtrlm_hip.so and need no CUDA
-    library.  Among them the callers SURVEY names: train_lm_gpu, generate,
+    library.  Among them the callers of the GPU path: train_lm_gpu, generate,
     chat, train_lm, train_faz4/5, data_parallel's tests, test_gpu_train and
     test_gpu_ops."""
     trlm.libs()

@@ -24,7 +24,8 @@ LIB_HIP = os.path.join(HERE, "libtrlm_hip.so")
 LIB_HOST = os.path.join(HERE, "libtrlm_host.so")
 NOALLOC_O = os.path.join(HERE, "noalloc.o")
 
-# Packed-fp32 VALU ops are disabled for all device code.
+# Packed-fp32 VALU ops are disabled for all device code: some of their forms
+# have given wrong results on the target boxes, without any error.
 HIPCC_FLAGS = ["--genco", "--offload-arch=gfx950", "-O3", "-Xclang", "-target-feature", "-Xclang",
                "-packed-fp32-ops"]
 CFLAGS = ["-std=c11", "-O2", "-fPIC", "-Wall", "-Wextra", "-Wno-unused-parameter", "-D_DEFAULT_SOURCE",
