@@ -17,9 +17,10 @@
 // Work split (causal blocks differ a lot in length: the last query block sees
 // every key): a workgroup owns 64 rows (queries, or keys for dK/dV) as two
 // 32-row groups, and each group's loop over the other axis is shared by two
-// wavefronts taking alternate 64-blocks.  The two partial results are merged
-// through LDS in a fixed order at the end, which halves the longest
-// per-wavefront loop without losing reproducibility.
+// wavefronts: in the forward and dQ passes each takes one 32-key half of
+// every 64-key block, in dK/dV alternate 64-query blocks.  The two partial
+// results are merged through LDS in a fixed order at the end, which halves
+// the longest per-wavefront loop without losing reproducibility.
 //
 // Layout: Q, K, V are read straight from qkv [B*T, ld] (head h at columns
 // h*HD, D+h*HD, 2D+h*HD, RoPE already applied) and O is written straight
@@ -528,29 +529,50 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
 
 // =========================================================== backward dQ
 // dQ_i = sum_{j <= i} dS_ij K_j from the dS blocks of the dK/dV pass.
-// grid (B*H, ceil(T/64)), 256 threads, three workgroups per CU, snake order
-// (att_snake_job: 49.5 against 54.7 us for plain longest-first at B8 T1024,
-// the same bits).  Wave w:
-// query group g = w&1 (32 queries), key partition part = w>>1 (key blocks
-// part, part+2, ...).  dQ^T accumulates as K^T dS^T: lane l feeds
+// grid (B*H, ceil(T/64)), 256 threads, snake order (att_snake_job).  Wave w:
+// query group g = w&1 (32 queries), key half part = w>>1: every stage takes
+// one 64-key block, part p its keys 32p .. 32p+31 (the stored dS key group
+// p), so the two parts always have equal work; their partial dQ^T merge
+// through LDS at the end.  dQ^T accumulates as K^T dS^T: lane l feeds
 // K[k][d0 + l%32] and dS[q + l%32][k] for k = 8c + 4(l/32) + s, so the dS
 // operand of four k-steps is one 128-bit load (four consecutive keys are
 // four consecutive lanes of the stored register rows).
+// The K tile goes straight from global memory into LDS (global_load_lds: no
+// staging registers, no transposing stores) in row-major [64][HD + 8] rows,
+// two buffers, one barrier per stage; the rows a wave's two halves read
+// together (4 apart) then sit 32 banks apart, and one ds_read2 gives both
+// 32-column d blocks of a k-step.  114 registers and 36 KB of LDS: four
+// workgroups fit a CU.  B8 T1024 hd64: 40.4 us against 49.5 for two key
+// blocks per stage with a transposed register-staged K tile (and 54.7 for
+// that form in plain longest-first order).
+typedef __attribute__((address_space(3))) void att_lds_void;
 template <int HD>
 __device__ void flash_bwd_dq_ds(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
-    __shared__ __attribute__((aligned(16))) float lds[2 * HD * ATT_LDT];
+    constexpr int LDK = HD + 8;                 // rows 4 apart are 32 banks apart
+    constexpr int TS = 64 * LDK;                // floats per K tile
+    constexpr int NCH = TS / 256;               // 1 KB global_load_lds chunks per tile
+    static_assert(TS % 256 == 0 && 2 * TS >= 2 * DB * 16 * 64, "K tile layout");
+    __shared__ __attribute__((aligned(16))) float lds[2 * TS];
 
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6, half = lane >> 5;
+    const int lane = threadIdx.x & 63, half = lane >> 5;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);   // wave-uniform
     const int grp = wave & 1, part = wave >> 1;
     const int nqb = (p.T + 63) / 64;
     int qb, bh;
     att_snake_job(nqb, qb, bh);
     const int b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
-    const float* qkv = p.qkv + rowbase * p.ldq;
-    const int qcol = h * HD, kcol = p.D + h * HD;
+    const float* kg = p.qkv + rowbase * p.ldq + p.D + h * HD;
+    const int qcol = h * HD;
     const int qpos = qb * 64 + grp * 32 + (lane & 31);
+    // this lane's query qq = l%32 of group grp sits in rows r(qq) of the
+    // (key group part, grp) sub-block, in lane half (qq/4)&1
+    const int qq = lane & 31;
+    const int ds_off = part * 2048 + grp * 1024 + ((qq >> 3) * 4 + (qq & 3)) * 64 + ((qq >> 2) & 1) * 32 + 4 * half;
+    const int nkv = qb + 1;
+    // lanes past HD (HD = 16) read column 0 of their row and feed 0
+    const int dl = (lane & 31) < HD ? (lane & 31) : 0;
 
     f32x16 acc[DB];
 #pragma unroll
@@ -558,56 +580,55 @@ __device__ void flash_bwd_dq_ds(const AttnParams& p) {
 #pragma unroll
         for (int r = 0; r < 16; r++) acc[d][r] = 0.f;
 
-    const int nkv = qb + 1;
-    const int niter = (nkv + 1) / 2;
-    const float* KT = lds + part * HD * ATT_LDT;
-    // this lane's query qq = l%32 of group grp sits in rows r(qq) of the
-    // (key group, grp) sub-blocks, in lane half (qq/4)&1
-    const int qq = lane & 31;
-    const int ds_off = grp * 1024 + ((qq >> 3) * 4 + (qq & 3)) * 64 + ((qq >> 2) & 1) * 32 + 4 * half;
-    // Software pipeline: the K tiles of stage it + 1 and this wave's dS block
-    // of that stage are loaded while stage it's MFMAs run.
-    AttTileT<HD> tk[2];
-    f32x4 sv[8];
-    tk[0].load(qkv, p.ldq, 0, p.T, kcol);
-    tk[1].load(qkv, p.ldq, 64, p.T, kcol);
-    if (part < nkv) {
-        const float* row = att_ds_block(p, bh, qb, part) + ds_off;
+    // K block kb into buf: chunk ci (256 floats) is one wave instruction,
+    // lane l the 16 bytes at float 256 ci + 4 l of the padded layout (pad
+    // columns take a copy of column 0, never read); rows past the end are
+    // clamped to the last row: their dS entries are exactly 0 (causal mask).
+    auto kload = [&](int kb, float* buf) {
+        for (int ci = wave; ci < NCH; ci += 4) {
+            const int pos = 256 * ci + 4 * lane;
+            const int r = pos / LDK, col = pos - r * LDK;
+            int key = kb * 64 + r;
+            key = key < p.T ? key : p.T - 1;
+            const float* src = kg + (long long)key * p.ldq + (col < HD ? col : 0);
+            __builtin_amdgcn_global_load_lds((const void*)src, (att_lds_void*)(buf + 256 * ci), 16, 0, 0);
+        }
+    };
+    auto sload = [&](int kb, f32x4* sv) {
+        const float* row = att_ds_block(p, bh, qb, kb) + ds_off;
 #pragma unroll
-        for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
-    }
-    for (int it = 0; it < niter; it++) {
-        // K of the stage's two key blocks, transposed ([HD][ATT_LDT]); rows
-        // past the end are stored as zeros
-        if (it > 0) __syncthreads();
-        tk[0].store(lds, 2 * it * 64, p.T);
-        tk[1].store(lds + HD * ATT_LDT, (2 * it + 1) * 64, p.T);
+        for (int c = 0; c < 4; c++) sv[c] = *(const f32x4*)(row + 8 * c);
+    };
+    auto mma = [&](const float* buf, const f32x4* sv) {
+        const float* kr = buf + (32 * part + 4 * half) * LDK + dl;
+#pragma unroll
+        for (int c = 0; c < 4; c++)
+#pragma unroll
+            for (int t = 0; t < 4; t++) {
+                const float* kp = kr + (8 * c + t) * LDK;
+#pragma unroll
+                for (int d = 0; d < DB; d++) {
+                    const float kv = (d * 32 + (lane & 31)) < HD ? kp[32 * d] : 0.f;
+                    acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(kv, sv[c][t], acc[d], 0, 0, 0);
+                }
+            }
+    };
+    // Stage kb: wait for this wave's loads of block kb, barrier (every wave's
+    // loads have landed, and every wave is done with the other buffer), issue
+    // block kb+1 into the other buffer, then the MFMAs of block kb.
+    f32x4 s0[4], s1[4];
+    kload(0, lds);
+    sload(0, s0);
+    for (int kb = 0; kb < nkv; kb += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
-        const int kb = 2 * it + part;
-        f32x4 cur[8];
-#pragma unroll
-        for (int c = 0; c < 8; c++) cur[c] = sv[c];
-        if (it + 1 < niter) {
-            tk[0].load(qkv, p.ldq, (2 * it + 2) * 64, p.T, kcol);
-            tk[1].load(qkv, p.ldq, (2 * it + 3) * 64, p.T, kcol);
-            if (kb + 2 < nkv) {
-                const float* row = att_ds_block(p, bh, qb, kb + 2) + ds_off;
-#pragma unroll
-                for (int c = 0; c < 8; c++) sv[c] = *(const f32x4*)(row + (c >> 2) * 2048 + 8 * (c & 3));
-            }
-        }
-        if (kb >= nkv) continue;
-#pragma unroll
-        for (int c = 0; c < 8; c++) {
-#pragma unroll
-            for (int d = 0; d < DB; d++) {
-                const int dc = d * 32 + (lane & 31);
-                const f32x4 ka = dc < HD ? *(const f32x4*)(KT + dc * ATT_LDT + 8 * c + 4 * half)
-                                         : f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-                for (int t = 0; t < 4; t++) acc[d] = __builtin_amdgcn_mfma_f32_32x32x2f32(ka[t], cur[c][t], acc[d], 0, 0, 0);
-            }
-        }
+        if (kb + 1 < nkv) { kload(kb + 1, lds + TS); sload(kb + 1, s1); }
+        mma(lds, s0);
+        if (kb + 1 >= nkv) break;
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (kb + 2 < nkv) { kload(kb + 2, lds); sload(kb + 2, s0); }
+        mma(lds + TS, s1);
     }
     __syncthreads();
     float* xch = lds + grp * (DB * 16 * 64);
