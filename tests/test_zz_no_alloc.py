@@ -70,7 +70,9 @@ def test_noalloc_equals_trlm_gemm_two_calls(trlm):
                        alpha=c["alpha"], beta=c["beta"], bias=up["bias"], resid=up["resid"], ldr=c["N"])
             want.append(ref.download(dC, (c["M"], c["N"])))
             plans.append(ref.last_variant())
-        assert plans[0][1] == 16 and plans[1][1] > 1, plans       # both take split-K (use the scratch)
+        # both take split-K (use the scratch), the second call's partials fewer
+        assert plans[0][1] > 1 and plans[1][1] > 1, plans
+        assert plans[1][1] * cases[1]["M"] * cases[1]["N"] < plans[0][1] * cases[0]["M"] * cases[0]["N"], plans
         dev.current()
         bufs = []
         for c in cases:

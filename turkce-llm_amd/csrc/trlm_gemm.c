@@ -148,7 +148,7 @@ static const PlanTile PLAN_TILES[] = {
     { T_128x128, 3, 1.047 }, { T_128x256, 2, 0.977 }, { T_256x128, 2, 1.008 },
     { T_64x128_K32, 2, 0.955 }, { T_64x64_K32, 4, 0.992 },
 };
-static const int PLAN_SPLITS[] = { 1, 2, 3, 4, 6, 8, 12, 16, 24, 32 };
+static const int PLAN_SPLITS[] = { 1, 2, 3, 4, 6, 7, 8, 12, 16, 24, 32 };
 #define PLAN_CU_FLOPS 0.6e12     /* per-CU steady-state fp32 MFMA rate, FLOP/s */
 #define PLAN_SPLIT_BW 1.63e12    /* effective bytes/s of the partials' round trip */
 #define PLAN_SPLIT_FIXED 1.25e-6 /* reduction launch, s */
