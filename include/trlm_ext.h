@@ -58,11 +58,15 @@ void trlm_gemm(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDevic
  * results (bit for bit) as trlm_gemm on an engine from trlm_gemm_create,
  * but the split-K partials go to a fixed 32 MiB scratch array that each GPU
  * holds from the first trlm_gemm_create on it until the process ends, so
- * the call allocates nothing.  Returns 0; or -1, with a message on stderr
- * and nothing launched, when the shape's split-K plan needs more than
- * 32 MiB (splits x (M+1) x N floats; of the model's GEMMs only the full-size
- * LM-head dX does).  All calls on one GPU share its scratch: calls that
- * overlap in time on one GPU (other streams, contexts or threads) race. */
+ * the call allocates nothing.  A plan whose partials need more than 32 MiB
+ * (splits x M x N floats; of the model's GEMMs only the full-size LM-head dX)
+ * runs with the most splits whose partials fit, down to one split, which
+ * needs none; its result then equals trlm_gemm on an engine forced to that
+ * split count (trlm_gemm_force(e, NULL, splits)), and trlm_gemm_last_variant
+ * reports it.  Returns 0; or -1, with a message on stderr and nothing
+ * launched, when the engine's device is not the calling thread's current
+ * device.  All calls on one GPU share its scratch: calls that overlap in time
+ * on one GPU (other streams, contexts or threads) race. */
 i32 trlm_gemm_noalloc(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                       i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                       f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr);
@@ -77,6 +81,10 @@ const char* trlm_gemm_plan(i32 trans_a, i32 trans_b, i32 M, i32 N, i32 K, u32 ba
  * factor (single GEMMs only).  tile NULL restores automatic selection.
  * Returns 0, or -1 for an unknown name (selection is then automatic). */
 i32 trlm_gemm_force(TrlmGemm* e, const char* tile, i32 splits);
+/* The GEMM engine of a trainer's main stream (the forward, the LM head and
+ * the backward's dX products), for trlm_gemm_force and
+ * trlm_gemm_last_variant. */
+TrlmGemm* gpu_trainer_gemm_engine(GpuTrainer* g);
 
 /* ---- checkpoints: TRLM v1 (training/checkpoint.h:6-12), the reference's
  * format and rules (checkpoint.c:22-137), straight from / to the device.

@@ -6,7 +6,8 @@ slide) that last row is what the decoder must produce, so:
   - after the prefill and after every step, the decoder's logits equal the
     oracle's full forward over the whole context at its last position, within
     1e-4 of max|logits| (head_dim 16, 32, 64; contexts crossing the
-    256-key chunks of the decode attention; batches 2 to 65);
+    256-key chunks of the decode attention; batches 2 to 65; d_model up to
+    512; d_ff not a multiple of 16);
   - greedy picks are the first maximum of those logits; generate_greedy
     equals prefill + greedy + step by hand, bit for bit;
   - sampling follows sample_next (generate.c:57-73) bit for bit: the oracle's
@@ -41,6 +42,8 @@ def last_rows(orc, model, params, ctx, B):
     (53, 32, 2, 1, 32, 65, 3, 2),      # batch 65
     (59, 96, 6, 2, 64, 3, 6, 4),       # six heads, odd batch: a workgroup with one sequence
     (61, 192, 12, 2, 96, 3, 5, 4),     # twelve heads of 16
+    (67, 512, 8, 1, 100, 3, 5, 4),     # d_model 512 (64 projection rows per wave, k_dec_head_k32), d_ff 100
+    (61, 448, 7, 2, 36, 2, 6, 4),      # d_model 448, seven heads; d_ff 36: partial 16-column blocks
 ])
 def test_decode_equals_full_recompute(trlm, orc, V, D, H, L, F, B, P, S):
     model = orc.Model(V, D, H, L, F)

@@ -73,12 +73,18 @@ def test_forward_loss_keeps_logits(trlm, orc, V, D, H, L, F, T, B):
     assert np.array_equal(am, host_argmax(logits2))
 
 
+GEMM_TILES = [None, "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
+
+
 @pytest.mark.parametrize("V,D,H,T,B", [(50, 32, 2, 12, 5), (1001, 32, 2, 64, 3), (31769, 64, 4, 128, 2)])
 def test_eval_loss_without_logits(trlm, orc, V, D, H, T, B):
     """eval_loss never writes the logits: the LM-head GEMM leaves the row
     statistics and each row's target logit.  Its loss must equal, bit for
     bit, the loss forward_loss_logits computes from stored logits, for
-    targets on tile and wave-column edges, the first and the last column."""
+    targets on tile and wave-column edges, the first and the last column --
+    with the plan's own tile and with each tile variant forced on the
+    trainer's GEMM engine, so that every variant's statistics and
+    target-logit epilogue (and its no-store path) is checked."""
     L, F = 2, 2 * D
     model = orc.Model(V, D, H, L, F)
     params = model.init(1337, 1)
@@ -88,11 +94,18 @@ def test_eval_loss_without_logits(trlm, orc, V, D, H, T, B):
     hm = trlm.HostModel(V, D, H, L, F, params)
     tr = trlm.Trainer(hm, B, T)
     try:
-        for k, targets in enumerate([tgt, np.zeros_like(tgt), np.full_like(tgt, V - 1),
-                                     np.resize(np.array(edges, np.uint32), tgt.size)]):
-            loss, _ = tr.forward_loss_logits(ids, targets)
-            ev = tr.eval_loss(ids, targets)
-            assert np.float32(loss).view(np.uint32) == np.float32(ev).view(np.uint32), (k, loss, ev)
+        for tile in GEMM_TILES:
+            tr.force_gemm(tile)
+            for k, targets in enumerate([tgt, np.zeros_like(tgt), np.full_like(tgt, V - 1),
+                                         np.resize(np.array(edges, np.uint32), tgt.size)]):
+                loss, _ = tr.forward_loss_logits(ids, targets, want_logits=False)
+                ev = tr.eval_loss(ids, targets)
+                head = tr.gemm_last_variant()[0]   # the LM head is the forward's last GEMM
+                assert head.startswith("k_gemm_nt_"), head
+                if tile is not None:
+                    assert head == "k_gemm_nt_" + tile, (tile, head)
+                assert np.float32(loss).view(np.uint32) == np.float32(ev).view(np.uint32), (tile, k, loss, ev)
+        tr.force_gemm(None)
         cpu_loss, _, _ = model.forward_backward(params, ids, tgt, B, T, want_grads=False)
         ev = tr.eval_loss(ids, tgt)
         assert abs(ev - cpu_loss) <= 1e-4 * abs(cpu_loss)

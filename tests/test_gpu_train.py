@@ -213,7 +213,12 @@ def test_overlap_equals_serial_at_config4(trlm, orc):
     weight-gradient work overlapped on the side stream gives the same loss and
     gradients, bit for bit, as the same kernels in one stream order -- at the
     real shape, where the side sections and the main chain run concurrently.
-    Then a rerun with overlap again repeats the first result."""
+    Then a rerun with overlap again repeats the first result.  Config 3's
+    timed path at the same shape: eval_loss (the LM-head GEMM leaves row
+    statistics and target logits and stores no logits) equals the
+    forward_backward loss bit for bit, with the plan's head tile and with
+    every tile variant forced (each against the stored-logits loss of
+    forward_loss_logits under the same tile)."""
     V, D, H, L, F, T, B = 31769, 384, 6, 12, 1024, 1024, 8
     model = orc.Model(V, D, H, L, F)
     params = model.init(1337, 1)
@@ -233,6 +238,17 @@ def test_overlap_equals_serial_at_config4(trlm, orc):
             hip.hip_side_serial(0)
         l3 = np.float32(tr.forward_backward(ids, tgt))
         g3 = tr.grads()
+        ev = np.float32(tr.eval_loss(ids, tgt))
+        head = tr.gemm_last_variant()
+        print("config 3 eval head: %s/split%d" % head)
+        forced = []
+        for tile in ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]:
+            tr.force_gemm(tile)
+            ev_t = np.float32(tr.eval_loss(ids, tgt))
+            assert tr.gemm_last_variant()[0] == "k_gemm_nt_" + tile
+            ls_t = np.float32(tr.forward_loss_logits(ids, tgt, want_logits=False)[0])
+            forced.append((tile, ev_t, ls_t))
+        tr.force_gemm(None)
     finally:
         tr.destroy()
         hm.close()
@@ -241,3 +257,7 @@ def test_overlap_equals_serial_at_config4(trlm, orc):
     assert l1.view(np.uint32) == l2.view(np.uint32) == l3.view(np.uint32)
     assert np.array_equal(g1.view(np.uint32), g2.view(np.uint32))
     assert np.array_equal(g1.view(np.uint32), g3.view(np.uint32))
+    assert ev.view(np.uint32) == l1.view(np.uint32), (ev, l1)
+    for tile, ev_t, ls_t in forced:
+        assert ev_t.view(np.uint32) == ls_t.view(np.uint32), (tile, ev_t, ls_t)
+        assert abs(float(ev_t) - float(l1)) <= 1e-5 * abs(float(l1)), (tile, ev_t, l1)

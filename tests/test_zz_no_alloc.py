@@ -1,14 +1,19 @@
 """trlm_gemm_noalloc: the raw GEMM with its split-K partials in the library's
 fixed 32 MiB scratch array instead of an allocated workspace.
 
-Through the C ABI, two calls in a row -- a weight-gradient shape whose
-split-K plan fills most of the scratch (384x1152x8192 TN, 16 splits,
-28.4 MB), then a smaller decode-sized one with the full epilogue (64 rows,
-alpha, beta*C, bias, residual) -- each equal to trlm_gemm's result on the
-same inputs bit for bit (same plan, same kernels), with the device's free
-memory unchanged across both calls; and a shape whose plan needs more than
-the scratch (the full LM-head dX, 100.7 MB) is refused with -1 and leaves C
-untouched.
+Through the C ABI:
+  - two calls in a row -- a weight-gradient shape that takes split-K
+    (384x1152x8192 TN: 7 splits, 12.4 MB of partials), then a smaller
+    decode-sized one with the full epilogue (64 rows, alpha, beta*C, bias,
+    residual) -- each equal to trlm_gemm's result on the same inputs bit for
+    bit (same plan, same kernels), with the device's free memory unchanged;
+  - the scratch boundary: with 8 splits forced on both engines, a
+    1024x1024 product whose partials fill exactly 32 MiB runs with its 8
+    splits, and a 1028x1024 one (32 MiB + 128 KiB) runs with the 7 splits
+    that fit, each equal bit for bit to trlm_gemm forced to that split count;
+  - the full-size LM-head dX (8192x384x31769 NN, planned with 8 splits,
+    100.7 MB of partials) runs with the 2 splits that fit, equal to
+    trlm_gemm forced to 2 splits.
 """
 import ctypes as C
 
@@ -99,18 +104,62 @@ def test_noalloc_equals_trlm_gemm_two_calls(trlm):
         assert np.array_equal(g.view(np.uint32), w.view(np.uint32))
 
 
-def test_noalloc_refuses_plans_beyond_the_scratch(trlm):
-    M, V, D, ld = 8192, 31769, 384, 31772
-    dev = trlm.Device()
+def _pair_run(trlm, c, splits_ref):
+    """trlm_gemm with splits_ref forced, and trlm_gemm_noalloc with the
+    engine's own plan (forced splits given as c['force']), on fresh
+    contexts; returns (want, got, ref plan, noalloc plan, free before,
+    free after)."""
+    ref, dev = trlm.Device(), trlm.Device()
     try:
-        dG = dev.empty(M * ld * 4)          # full-size operands: nothing may be read even if launched
-        dE = dev.empty(V * D * 4)
-        C0 = np.full((M, D), 3.0, np.float32)
-        dC = dev.upload(C0)
-        rc = dev.matmul_noalloc(0, 0, dG, dE, dC, M, D, V, ld, D, D)
+        ref.current()
+        ref.force(None, splits_ref)
+        up = _upload(ref, c)
+        dC = ref.upload(c["C0"])
+        lda, ldb = _lds(c)
+        ref.matmul(c["ta"], c["tb"], up["A"], up["B"], dC, c["M"], c["N"], c["K"], lda, ldb, c["N"])
+        want = ref.download(dC, (c["M"], c["N"]))
+        plan_ref = ref.last_variant()
+        dev.current()
+        dev.force(None, c["force"])
+        up = _upload(dev, c)
+        dC = dev.upload(c["C0"])
         dev.sync()
-        got = dev.download(dC, (M, D))
+        before = _free_bytes()
+        rc = dev.matmul_noalloc(c["ta"], c["tb"], up["A"], up["B"], dC, c["M"], c["N"], c["K"], lda, ldb, c["N"])
+        dev.sync()
+        after = _free_bytes()
+        assert rc == 0
+        got = dev.download(dC, (c["M"], c["N"]))
+        plan = dev.last_variant()
     finally:
         dev.close()
-    assert rc == -1
-    assert np.array_equal(got, C0)
+        ref.close()
+    return want, got, plan_ref, plan, before, after
+
+
+@pytest.mark.parametrize("M,fit", [(1024, 8), (1028, 7)])
+def test_noalloc_scratch_boundary(trlm, M, fit):
+    rng = np.random.default_rng(11)
+    c = _case(rng, 1, 0, M, 1024, 2048, False)
+    c["force"] = 8
+    assert (8 * M * 1024 <= (32 << 20) // 4) == (fit == 8)
+    want, got, plan_ref, plan, before, after = _pair_run(trlm, c, fit)
+    assert plan_ref[1] == fit and plan == plan_ref, (plan_ref, plan)
+    assert after == before, (before, after)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+def test_noalloc_caps_the_lm_head_dx(trlm):
+    M, V, D, ldv = 8192, 31769, 384, 31772   # the trainer's logits rows are padded to 16 bytes
+    rng = np.random.default_rng(5)
+    c = dict(ta=0, tb=0, M=M, N=D, K=V, A=rng.standard_normal((M, ldv), dtype=np.float32) * np.float32(1e-4),
+             B=rng.standard_normal((V, D), dtype=np.float32) * np.float32(0.02), C0=np.zeros((M, D), np.float32),
+             bias=None, resid=None, force=0)
+    _, hip = trlm.libs()
+    sp = C.c_int32(0)
+    hip.trlm_gemm_plan(0, 0, M, D, V, 1, C.byref(sp))
+    assert sp.value * M * D * 4 > (32 << 20), sp.value   # the plan's own partials do not fit
+    want, got, plan_ref, plan, before, after = _pair_run(trlm, c, 2)
+    assert plan_ref[1] == 2 and plan == plan_ref, (plan_ref, plan)
+    assert after == before, (before, after)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))

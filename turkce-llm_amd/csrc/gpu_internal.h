@@ -73,13 +73,16 @@ i32 trlm_gemm_ex(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
                  f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x);
 
 /* trlm_gemm_ex with the split-K partials in a caller-given workspace of
- * fixed_floats floats (fixed_ws != NULL): no allocation; returns -1, having
- * launched nothing, when the plan needs more.  fixed_ws == NULL is
- * trlm_gemm_ex (the engine's grow-only workspace). */
+ * fixed_floats floats (fixed_ws != NULL): no allocation; a plan whose
+ * partials do not fit runs with the most splits that do (down to one split,
+ * which needs no workspace), as if forced to that count.  fixed_ws == NULL
+ * is trlm_gemm_ex (the engine's grow-only workspace). */
 i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDeviceptr_t B, hipDeviceptr_t C,
                  i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA, i64 sB, i64 sC,
                  f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid, i32 ldr, const TrlmGemmExtra* x,
                  hipDeviceptr_t fixed_ws, u64 fixed_floats);
+/* The device of the context the engine was created in. */
+i32 trlm_gemm_device(const TrlmGemm* e);
 /* noalloc.hip: resolves the device address of the GEMM scratch array on
  * `device` (once per device; trlm_gemm_create calls it). */
 void trlm_noalloc_setup(i32 device);

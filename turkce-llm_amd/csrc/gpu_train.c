@@ -833,6 +833,11 @@ void gpu_trainer_adamw_step_scaled(GpuTrainer* g, AdamOptimizer* opt, f32 weight
     adam_launch(g, opt, grad_scale, weight_decay);
 }
 
+TrlmGemm* gpu_trainer_gemm_engine(GpuTrainer* g) {
+    bind(g);
+    return g->gemm;
+}
+
 /* ---------------- helpers shared with the decoder (gpu_decode.c) ---------------- */
 
 void trlm_bind(GpuTrainer* g) { bind(g); }

@@ -11,6 +11,8 @@
 // current, and only that address is handed to kernels or copies; the array's
 // name is host-side only.
 //
+// A plan whose partials exceed the scratch runs with the most splits whose
+// partials fit (one split needs none), as trlm_gemm forced to that count.
 // Every split writes its whole slab of partials before the ordered
 // reduction reads it, so nothing in scratch needs clearing between calls.
 // All calls on one GPU share its scratch: calls that overlap in time on one
@@ -61,12 +63,24 @@ extern "C" i32 trlm_gemm_noalloc(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDevic
                                  hipDeviceptr_t C, i32 M, i32 N, i32 K, i32 lda, i32 ldb, i32 ldc, u32 batch, i64 sA,
                                  i64 sB, i64 sC, f32 alpha, f32 beta, hipDeviceptr_t bias, hipDeviceptr_t resid,
                                  i32 ldr) {
-    int device = 0;
-    hipError_t r = hipGetDevice(&device);
+    // The scratch copy is the one of the engine's device, and its kernels
+    // must run there: a thread that made another device current is refused.
+    const i32 device = trlm_gemm_device(e);
+    int cur = -1;
+    hipError_t r = hipGetDevice(&cur);
     if (r != hipSuccess) noalloc_fatal("hipGetDevice", r);
+    if (cur != device) {
+        fprintf(stderr,
+                "trlm_gemm_noalloc: refused, nothing launched: the engine belongs to device %d, device %d is current\n",
+                device, cur);
+        fflush(stderr);
+        return -1;
+    }
+    pthread_mutex_lock(&scratch_lock);
     void* ws = (device >= 0 && device < TRLM_MAX_DEVICES) ? scratch_dev[device] : NULL;
+    pthread_mutex_unlock(&scratch_lock);
     if (!ws) {
-        fprintf(stderr, "[HIP ERROR] trlm_gemm_noalloc: no GEMM engine was created on device %d\n", device);
+        fprintf(stderr, "[HIP ERROR] trlm_gemm_noalloc: no scratch address for device %d\n", device);
         fflush(stderr);
         _exit(1);
     }

@@ -80,6 +80,8 @@ void trlm_gemm_destroy(TrlmGemm* e) {
     free(e);
 }
 
+i32 trlm_gemm_device(const TrlmGemm* e) { return e->ctx->device; }
+
 const char* trlm_gemm_last_variant(TrlmGemm* e, i32* splits) {
     if (splits) *splits = e->last_splits;
     return e->last;
@@ -336,28 +338,31 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
         kchunk = cdiv(cdiv(K, splits), KCHUNK_ALIGN) * KCHUNK_ALIGN;
         splits = cdiv(K, kchunk);
     }
+    /* split-K: raw partials into the workspace, then an ordered reduction;
+     * with column sums each split's slab has one more row, M, for them */
+    u64 slab = ((u64)M + (csum ? 1u : 0u)) * (u64)N;
+    if (fixed_ws && splits > 1 && (u64)splits * slab > fixed_floats) {
+        /* A fixed workspace that cannot hold the plan's partials: run the
+         * most splits whose partials fit (one split needs none).  The k
+         * chunks are formed as for a forced split count, so the result
+         * equals this engine's trlm_gemm forced to that many splits. */
+        u64 fit = fixed_floats / slab;
+        splits = fit < 2 ? 1 : (int)fit;
+        kchunk = K;
+        if (splits > 1) {
+            kchunk = cdiv(cdiv(K, splits), KCHUNK_ALIGN) * KCHUNK_ALIGN;
+            splits = cdiv(K, kchunk);
+        }
+    }
     snprintf(e->last, sizeof(e->last), "k_gemm_%s_%s", LAYOUT_NAME[layout], TILES[tile].name);
     e->last_splits = splits;
     if (splits <= 1) {
         launch(e->k[layout][tile], &p, batch);
         return p.stats ? 2 * p.tiles_n : 0;
     }
-    /* split-K: raw partials into the workspace, then an ordered reduction;
-     * with column sums each split's slab has one more row, M, for them */
-    u64 slab = ((u64)M + (csum ? 1u : 0u)) * (u64)N;
     u64 need = (u64)splits * slab;
     hipDeviceptr_t W = fixed_ws;
-    if (fixed_ws) {
-        if (need > fixed_floats) {
-            fprintf(stderr,
-                    "[HIP ERROR] trlm_gemm_noalloc: %s with %d K splits needs %llu bytes of split-K workspace, "
-                    "more than the %llu-byte scratch; nothing was launched\n",
-                    e->last, splits, (unsigned long long)(need * sizeof(f32)),
-                    (unsigned long long)(fixed_floats * sizeof(f32)));
-            fflush(stderr);
-            return -1;
-        }
-    } else {
+    if (!fixed_ws) {
         if (need > e->ws_floats) {
             if (e->ws) hip_free(e->ws);
             e->ws = hip_alloc(need * sizeof(f32));

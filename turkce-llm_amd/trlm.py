@@ -172,6 +172,7 @@ def _bind(host, hip):
     _sig(hip, "gpu_trainer_forward_logits", None, [GP, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_forward_loss_logits", C.c_float, [GP, u32p, u32p, C.c_void_p])
     _sig(hip, "gpu_trainer_greedy_argmax", None, [GP, u32p])
+    _sig(hip, "gpu_trainer_gemm_engine", C.c_void_p, [GP])
     ckpt_args = [GP, C.c_char_p, C.POINTER(NodeP), C.POINTER(AdamOptimizer)]
     _sig(hip, "gpu_trainer_checkpoint_save", C.c_uint32, ckpt_args)
     _sig(hip, "gpu_trainer_checkpoint_load", C.c_uint32, ckpt_args)
@@ -438,6 +439,20 @@ class Trainer:
         self.hip.gpu_trainer_greedy_argmax(C.byref(self.g), out)
         return out
 
+    def force_gemm(self, tile=None, splits=0):
+        """trlm_gemm_force on the trainer's main-stream GEMM engine: later
+        forward, LM-head and dX products use that tile variant (None restores
+        automatic selection)."""
+        eng = self.hip.gpu_trainer_gemm_engine(C.byref(self.g))
+        if self.hip.trlm_gemm_force(eng, tile.encode() if tile else None, splits) != 0:
+            raise ValueError("unknown GEMM tile variant %r" % tile)
+
+    def gemm_last_variant(self):
+        """(kernel, splits) of the main engine's last GEMM."""
+        eng = self.hip.gpu_trainer_gemm_engine(C.byref(self.g))
+        sp = C.c_int32(0)
+        return self.hip.trlm_gemm_last_variant(eng, C.byref(sp)).decode(), sp.value
+
     def destroy(self):
         if self.g is not None:
             self.hip.gpu_trainer_destroy(C.byref(self.g))
@@ -535,8 +550,9 @@ class Device:
 
     def matmul_noalloc(self, ta, tb, A, B, C_, M, N, K, lda, ldb, ldc, batch=1, sA=0, sB=0, sC=0, alpha=1.0,
                        beta=0.0, bias=None, resid=None, ldr=0):
-        """trlm_gemm_noalloc: returns 0, or -1 when the plan's split-K
-        workspace exceeds the 32 MiB scratch (nothing launched)."""
+        """trlm_gemm_noalloc: returns 0 (a plan whose split-K partials
+        exceed the 32 MiB scratch runs with the most splits that fit), or -1
+        when the engine's device is not the current one (nothing launched)."""
         return self.hip.trlm_gemm_noalloc(self.gemm, ta, tb, A, B, C_, M, N, K, lda, ldb, ldc, batch, sA, sB, sC,
                                           alpha, beta, bias, resid, ldr or ldc)
 
