@@ -243,6 +243,7 @@ def hybrid_benchmarks(trlm, reps=10):
 
 
 DEC_B, DEC_PROMPT, DEC_CTX = 64, 128, 1024
+DEC_TEMP = 0.85   # generate.c:54 TEMPERATURE
 
 
 def decode_benchmark(trlm):
@@ -250,7 +251,9 @@ def decode_benchmark(trlm):
     pcg_seed(4242, 9)), greedy KV-cache decode to context 1024: 896 new tokens
     per sequence (prefill + 895 steps), random-init weights of the real
     architecture.  Bytes per step = all weights (133.96 MB) + the K and V
-    cache read by the step (64*12*2*ctx*384*4 B)."""
+    cache read by the step (64*12*2*ctx*384*4 B).  The same generation
+    sampled (sample_next at temperature 0.85, one PCG stream per sequence) is
+    timed as decode_sampled_*."""
     host, _ = trlm.libs()
     import ctypes as C
     rng = np.random.default_rng(11)
@@ -267,6 +270,14 @@ def decode_benchmark(trlm):
         t0 = time.perf_counter()
         dec.generate_greedy(prompt, steps)
         dt = time.perf_counter() - t0
+        # sampled generation (the reference's generate.c: sample_next at TEMPERATURE 0.85), one PCG
+        # stream per sequence, pcg_seed(4242, 7 + b) (the reference's single stream is (4242, 7))
+        rngs = (trlm.PCGState * DEC_B)(*[host.pcg_seed(4242, 7 + b) for b in range(DEC_B)])
+        dec.generate_sampled(prompt, 16, rngs, DEC_TEMP)
+        rngs = (trlm.PCGState * DEC_B)(*[host.pcg_seed(4242, 7 + b) for b in range(DEC_B)])
+        t0 = time.perf_counter()
+        dec.generate_sampled(prompt, steps, rngs, DEC_TEMP)
+        dts = time.perf_counter() - t0
     finally:
         dec.destroy()
         tr.destroy()
@@ -277,6 +288,8 @@ def decode_benchmark(trlm):
     tokens = DEC_B * steps
     return {"decode_tokens_per_s": tokens / dt, "decode_ms_per_token": dt * 1e3 / steps,
             "decode_gbps": total / dt / 1e9, "decode_total_s": dt,
+            "decode_sampled_tokens_per_s": tokens / dts, "decode_sampled_ms_per_token": dts * 1e3 / steps,
+            "decode_sampled_temperature": DEC_TEMP,
             "decode_config": "batch %d, prompt %d, greedy to context %d (%d steps)" % (
                 DEC_B, DEC_PROMPT, DEC_CTX, steps - 1)}
 

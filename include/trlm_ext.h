@@ -122,6 +122,14 @@ void gpu_decoder_sample(TrlmDecoder* d, PCGState* rngs, f32 temperature, u32* ou
 /* prefill + greedy generation of `steps` tokens per sequence; out
  * [batch][steps] (prompt_len + steps <= max_ctx) */
 void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, u32* out);
+/* prefill + sampled generation (sample_next at `temperature`, generate.c:
+ * 57-73,186-212, without its end-of-text stop): out [batch][steps], the same
+ * picks as prefill + (gpu_decoder_sample, gpu_decoder_step) per token, with
+ * rngs[b] advanced by one pcg_uniform per token of sequence b as the
+ * reference's loop draws them (all drawn up front; no host round trip per
+ * token) */
+void gpu_decoder_generate_sampled(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, PCGState* rngs,
+                                  f32 temperature, u32* out);
 
 /* ---- training driver loop (training/train_lm_gpu.c:212-223, 241-258) ----
  * The reference's driver, per step: lr = lr_warmup_cosine(step, ...);

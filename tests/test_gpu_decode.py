@@ -12,7 +12,10 @@ slide) that last row is what the decoder must produce, so:
     equals prefill + greedy + step by hand, bit for bit;
   - sampling follows sample_next (generate.c:57-73) bit for bit: the oracle's
     restatement, run on the decoder's own logits with the same PCG streams,
-    picks the same tokens and leaves the streams in the same state;
+    picks the same tokens and leaves the streams in the same state, both on
+    the kernel's parallel exact-prefix path and on its sequential path, at
+    the real vocabulary and temperatures 0.05 to 2 (and 0); sampled
+    generation on the device equals the per-token loop;
   - at the real architecture (V 31769, D 384, L 12) the decoder equals the
     GPU trainer's full forward (itself pinned to the oracle) at the last
     position, within 1e-4.
@@ -126,6 +129,132 @@ def test_sampling_follows_sample_next(trlm, orc):
         dec.destroy()
         tr.destroy()
         hm.close()
+
+
+def test_generate_sampled_matches_manual_loop(trlm, orc):
+    """gpu_decoder_generate_sampled draws every uniform up front and samples
+    on the device: the same picks as prefill + (sample, step) per token, bit
+    for bit, and the PCG streams end in the same state."""
+    V, D, H, L, F, B, P, S = 97, 64, 2, 2, 96, 3, 6, 9
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    d1 = trlm.Decoder(tr, B, P + S)
+    d2 = trlm.Decoder(tr, B, P + S)
+    seed = lambda: (trlm.PCGState * B)(*[trlm.libs()[0].pcg_seed(4242, 7 + b) for b in range(B)])
+    r1, r2 = seed(), seed()
+    try:
+        gen = d1.generate_sampled(prompt, S, r1, 0.85)
+        d2.prefill(prompt)
+        manual = []
+        for s in range(S):
+            nxt = d2.sample(r2, 0.85)
+            manual.append(nxt)
+            if s + 1 < S:
+                d2.step(nxt)
+        assert np.array_equal(gen, np.stack(manual, axis=1)), (gen, np.stack(manual, axis=1))
+        for b in range(B):
+            assert r1[b].state == r2[b].state and r1[b].inc == r2[b].inc
+    finally:
+        d1.destroy()
+        d2.destroy()
+        tr.destroy()
+        hm.close()
+
+
+@pytest.mark.parametrize("temp", [0.85, 0.05, 2.0, 0.0])
+def test_sampling_parallel_decision_equals_sequential_sums(trlm, orc, temp, monkeypatch):
+    """At the real vocabulary (V 31,769), batch 64: the kernel's parallel
+    exact-prefix decision picks what the reference's sequential f64 sums pick
+    -- the same kernel forced onto its sequential path
+    (TRLM_SAMPLE_SEQUENTIAL=1) and the oracle's sample_next on the same
+    logits and PCG streams -- for three decode positions; temperature 0.05
+    spreads the probabilities over hundreds of binades (most terms far below
+    the running sum's rounding), 0 makes every sum NaN (the reference then
+    returns the last index)."""
+    V, D, H, L, F, B, P = 31769, 64, 2, 1, 64, 64, 4
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    params[:V * D] *= np.float32(20.0)    # the tied head's rows: logits of a few units, not ~0.2
+    prompt = orc.random_tokens(B * P, V, 4242, 9).reshape(B, P)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, B, P + 4)
+    seeds = lambda: (trlm.PCGState * B)(*[trlm.libs()[0].pcg_seed(99, b) for b in range(B)])
+    ra, rb = seeds(), seeds()
+    mirror = [orc.pcg_stream(99, b) for b in range(B)]
+    try:
+        dec.prefill(prompt)
+        for step in range(3):
+            logits = dec.logits()
+            fast = dec.sample(ra, temp)
+            monkeypatch.setenv("TRLM_SAMPLE_SEQUENTIAL", "1")
+            seq = dec.sample(rb, temp)
+            monkeypatch.delenv("TRLM_SAMPLE_SEQUENTIAL")
+            want = [orc.sample_next(logits[b], temp, mirror[b]) for b in range(B)]
+            assert list(seq) == want, (step, list(seq), want)
+            assert list(fast) == want, (step, list(fast), want)
+            dec.step(fast)
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+
+
+@pytest.mark.parametrize("temp", [1.0, 0.37])
+def test_sample_exponentials_equal_m_expf(trlm, orc, temp):
+    """k_sample_exp's e_j = m_expf((z_j - max) / temperature) bit for bit
+    against the oracle's m_expf (the reference's f64 Taylor series), over
+    64 rows x 31,769 inputs spanning [-120, 0]: both sides of the -110
+    cut-off and of float underflow (exp(x) ~ 2^-150), exact 0, and inputs
+    whose exp lies within 1e-13 of a midpoint between two floats (where the
+    kernel evaluates the series itself instead of its fast polynomial)."""
+    import ctypes as C
+    rows, V = 64, 31769
+    ld = (V + 3) // 4 * 4
+    rng = np.random.default_rng(3)
+    z = rng.uniform(-120.0 * temp, 0.0, size=(rows, V)).astype(np.float32)
+    z[:, 0] = 0.0                                          # the row max
+    specials = np.array([-0.0, -1e-30, -110.0, -109.99999, -110.00001, -103.2789, -103.9721, -104.5, -87.33655,
+                         -0.6931472, -0.34657359, -745.2, -1e-7], np.float32)
+    z[0, 1:1 + specials.size] = specials * np.float32(temp)
+    # inputs whose exp is within 1e-13 (relative) of a float rounding midpoint
+    cand = rng.uniform(-103.0, 0.0, size=4_000_000)
+    cand = cand.astype(np.float32).astype(np.float64)
+    y = np.exp(cand)
+    f = y.astype(np.float32).astype(np.float64)
+    up = np.nextafter(y.astype(np.float32), np.float32(np.inf)).astype(np.float64)
+    dn = np.nextafter(y.astype(np.float32), np.float32(0)).astype(np.float64)
+    mid = np.where(y >= f, 0.5 * (f + up), 0.5 * (f + dn))
+    near = cand[np.abs(y - mid) < 1e-13 * y].astype(np.float32)
+    assert near.size >= 3, near.size
+    z[1, 1:1 + near.size] = near * np.float32(temp)
+    x = ((z - z.max(axis=1, keepdims=True)) / np.float32(temp)).astype(np.float32)
+    m_expf = orc.lib().or_m_expf
+    want = np.array([[m_expf(float(v)) for v in row] for row in x[:2]], np.float32)
+    pad = np.zeros((rows, ld), np.float32)
+    pad[:, :V] = z
+    _, hip = trlm.libs()
+    dev = trlm.Device()
+    try:
+        dz, de = dev.upload(pad), dev.empty(rows * ld * 4)
+        f_ = hip.hip_get_kernel(C.byref(dev.ctx), b"k_sample_exp")
+        pz, pe = C.c_void_p(dz), C.c_void_p(de)
+        cl, cv, ct = C.c_int32(ld), C.c_int32(V), C.c_float(temp)
+        args = (C.c_void_p * 5)(C.addressof(pz), C.addressof(cl), C.addressof(cv), C.addressof(ct), C.addressof(pe))
+        hip.hip_launch(f_, 8, rows, 1, 1024, 1, 1, 0, args)
+        got = dev.download(de, (rows, ld))[:, :V]
+    finally:
+        dev.close()
+    assert np.array_equal(got[:2].view(np.uint32), want.view(np.uint32))
+    # the other rows: the same function, checked on a seeded sample of columns
+    idx = rng.integers(0, V, size=4000)
+    for r in range(2, rows, 7):
+        w = np.array([m_expf(float(v)) for v in x[r, idx]], np.float32)
+        assert np.array_equal(got[r, idx].view(np.uint32), w.view(np.uint32)), r
+    print("near-midpoint inputs: %d" % near.size)
 
 
 def test_real_architecture_against_gpu_full_forward(trlm, orc):

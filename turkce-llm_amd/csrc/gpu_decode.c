@@ -55,7 +55,9 @@ struct TrlmDecoder {
     /* prefill buffers, grown to batch x len rows on demand */
     u64 pre_rows;
     hipDeviceptr_t p_x, p_x2, p_n, p_r1, p_r2, p_qkv, p_att, p_lse, p_gu, p_h, p_nf, p_rf, p_ids;
-    hipFunction_t k_fill, k_gather, k_sample, k_argmax_hist;
+    hipFunction_t k_fill, k_gather, k_sample_exp, k_sample, k_sample_hist, k_argmax_hist;
+    hipDeviceptr_t u_all;                /* sampled generation: the uniforms of every step */
+    u64 u_cap;
     hipFunction_t k_qkv_attn, k_out, k_gu, k_down, k_head;
     /* step replay: the position lives on the device (pos_dev), so every step
      * is the same launch sequence -- captured once as a HIP graph on the
@@ -111,7 +113,7 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     d->logits = fl(B * g->ldv);
     hip_memset_zero(d->logits, B * g->ldv * F4);
     d->out_ids = hip_alloc(B * sizeof(u32));
-    d->e = fl(B * g->V);
+    d->e = fl(B * g->ldv);
     d->prefix = hip_alloc(B * g->V * sizeof(f64));
     d->u = hip_alloc(B * sizeof(f64));
 
@@ -142,7 +144,9 @@ TrlmDecoder* gpu_decoder_create(GpuTrainer* g, u32 batch, u32 max_ctx) {
     char name[64];
     d->k_fill = hip_get_kernel(c, "k_cache_fill");
     d->k_gather = hip_get_kernel(c, "k_gather_rows");
+    d->k_sample_exp = hip_get_kernel(c, "k_sample_exp");
     d->k_sample = hip_get_kernel(c, "k_sample_rows");
+    d->k_sample_hist = hip_get_kernel(c, "k_sample_hist");
     d->k_argmax_hist = hip_get_kernel(c, "k_argmax_hist");
     d->k_out = hip_get_kernel(c, "k_dec_out");
     d->k_gu = hip_get_kernel(c, "k_dec_gu");
@@ -177,6 +181,7 @@ void gpu_decoder_destroy(TrlmDecoder* d) {
     drop_graph(d);
     free_prefill(d);
     if (d->hist) hip_free(d->hist);
+    if (d->u_all) hip_free(d->u_all);
     hip_free(d->pos_dev);
     hipDeviceptr_t bufs[] = { d->kc, d->vc, d->ids, d->x, d->x2, d->att, d->h, d->nf,
                               d->logits, d->out_ids, d->e, d->prefix, d->u, d->cos_t, d->sin_t };
@@ -406,29 +411,90 @@ void gpu_decoder_greedy(TrlmDecoder* d, u32* out_ids) {
     hip_d2h(out_ids, d->out_ids, (u64)d->B * sizeof(u32));
 }
 
+#define DEC_SAMPLE_THREADS 1024u   /* threads per workgroup of the sampling kernels */
+#define DEC_SAMPLE_CHUNKS 8u       /* k_sample_exp workgroups per row (as in decode.hip) */
+
+/* e = sample_next's exponentials of every row of the current logits */
+static void sample_exp(TrlmDecoder* d, f32 temperature) {
+    hipDeviceptr_t lg = d->logits, e = d->e;
+    i32 ld = (i32)d->ldv, V = (i32)d->V;
+    void* args[] = { &lg, &ld, &V, &temperature, &e };
+    hip_launch(d->k_sample_exp, DEC_SAMPLE_CHUNKS, d->B, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
+}
+
+/* TRLM_SAMPLE_SEQUENTIAL=1: every row takes the kernel's sequential path
+ * (the reference's f64 sums on one thread) instead of the parallel exact
+ * decision -- for checking that the two agree. */
+static i32 sample_sequential(void) {
+    const char* e = getenv("TRLM_SAMPLE_SEQUENTIAL");
+    return (e && e[0] == '1') ? 1 : 0;
+}
+
 void gpu_decoder_sample(TrlmDecoder* d, PCGState* rngs, f32 temperature, u32* out_ids) {
     trlm_bind(d->g);
     f64* u = (f64*)malloc((u64)d->B * sizeof(f64));
     if (!u) dec_fatal("out of host memory");
     for (u32 b = 0; b < d->B; b++) u[b] = (f64)pcg_next_u32(&rngs[b]) * (1.0 / 4294967296.0);   /* pcg_uniform */
     hip_h2d(d->u, u, (u64)d->B * sizeof(f64));
-    hipDeviceptr_t lg = d->logits, e = d->e, pr = d->prefix, up = d->u, out = d->out_ids;
-    i32 ld = (i32)d->ldv, V = (i32)d->V;
-    void* args[] = { &lg, &ld, &V, &temperature, &up, &e, &pr, &out };
-    hip_launch(d->k_sample, d->B, 1, 1, 256, 1, 1, 0, args);
+    hipDeviceptr_t e = d->e, pr = d->prefix, up = d->u, out = d->out_ids;
+    i32 V = (i32)d->V, ld = (i32)d->ldv, seq = sample_sequential();
+    void* args[] = { &V, &ld, &up, &e, &pr, &out, &seq };
+    sample_exp(d, temperature);
+    hip_launch(d->k_sample, d->B, 1, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
     hip_d2h(out_ids, d->out_ids, (u64)d->B * sizeof(u32));
     free(u);
+}
+
+/* History buffer of `steps` picks per sequence (grow-only). */
+static void ensure_hist(TrlmDecoder* d, u32 steps) {
+    if (d->hist_cap < d->B * steps) {
+        if (d->hist) hip_free(d->hist);
+        d->hist = hip_alloc((u64)d->B * steps * sizeof(u32));
+        d->hist_cap = d->B * steps;
+    }
+}
+
+void gpu_decoder_generate_sampled(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, PCGState* rngs,
+                                  f32 temperature, u32* out) {
+    if (steps == 0) return;
+    if ((u64)prompt_len + steps > d->ctx) dec_fatal("prompt_len + steps exceeds max_ctx");
+    gpu_decoder_prefill(d, prompt, prompt_len);
+    ensure_hist(d, steps);
+    /* every uniform up front, in the order the reference's loop draws them:
+     * one pcg_uniform per sequence and token, from that sequence's stream */
+    u64 n = (u64)steps * d->B;
+    f64* u = (f64*)malloc(n * sizeof(f64));
+    if (!u) dec_fatal("out of host memory");
+    for (u32 s = 0; s < steps; s++)
+        for (u32 b = 0; b < d->B; b++) u[(u64)s * d->B + b] = (f64)pcg_next_u32(&rngs[b]) * (1.0 / 4294967296.0);
+    if (d->u_cap < n) {
+        if (d->u_all) hip_free(d->u_all);
+        d->u_all = hip_alloc(n * sizeof(f64));
+        d->u_cap = n;
+    }
+    hip_h2d(d->u_all, u, n * sizeof(f64));
+    free(u);
+    /* pick s is taken when *pos_dev = prompt_len + s; it becomes the ids of
+     * the next step directly on the device */
+    hipDeviceptr_t ua = d->u_all, e = d->e, pr = d->prefix, ids = d->ids, hist = d->hist, posd = d->pos_dev;
+    i32 V = (i32)d->V, ld = (i32)d->ldv, hl = (i32)steps, base = (i32)prompt_len, seq = sample_sequential();
+    void* args[] = { &V, &ld, &ua, &e, &pr, &ids, &hist, &hl, &posd, &base, &seq };
+    sample_exp(d, temperature);
+    hip_launch(d->k_sample_hist, d->B, 1, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
+    for (u32 s = 1; s < steps; s++) {
+        run_step(d);
+        d->len++;
+        sample_exp(d, temperature);
+        hip_launch(d->k_sample_hist, d->B, 1, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
+    }
+    hip_d2h(out, d->hist, (u64)d->B * steps * sizeof(u32));
 }
 
 void gpu_decoder_generate_greedy(TrlmDecoder* d, const u32* prompt, u32 prompt_len, u32 steps, u32* out) {
     if (steps == 0) return;
     if ((u64)prompt_len + steps > d->ctx) dec_fatal("prompt_len + steps exceeds max_ctx");
     gpu_decoder_prefill(d, prompt, prompt_len);
-    if (d->hist_cap < d->B * steps) {
-        if (d->hist) hip_free(d->hist);
-        d->hist = hip_alloc((u64)d->B * steps * sizeof(u32));
-        d->hist_cap = d->B * steps;
-    }
+    ensure_hist(d, steps);
     /* pick s (s = 0 .. steps-1) is taken when *pos_dev = prompt_len + s; it
      * becomes the ids of the next step directly on the device */
     hipDeviceptr_t lg = d->logits, ids = d->ids, hist = d->hist, posd = d->pos_dev;

@@ -192,6 +192,8 @@ def _bind(host, hip):
     _sig(hip, "gpu_decoder_greedy", None, [DP, u32p])
     _sig(hip, "gpu_decoder_sample", None, [DP, C.POINTER(PCGState), C.c_float, u32p])
     _sig(hip, "gpu_decoder_generate_greedy", None, [DP, u32p, C.c_uint32, C.c_uint32, u32p])
+    _sig(hip, "gpu_decoder_generate_sampled", None, [DP, u32p, C.c_uint32, C.c_uint32, C.POINTER(PCGState),
+                                                     C.c_float, u32p])
 
     HP = C.POINTER(HipCtx)
     _sig(hip, "hip_init", HipCtx, [AP, C.c_char_p])
@@ -498,6 +500,13 @@ class Decoder:
         prompt = _u32(prompt)
         out = np.zeros((self.B, steps), np.uint32)
         self.hip.gpu_decoder_generate_greedy(self.d, prompt.ravel(), prompt.shape[-1], steps, out)
+        return out
+
+    def generate_sampled(self, prompt, steps, rngs, temperature):
+        """rngs: ctypes array of PCGState (one per sequence), advanced in place."""
+        prompt = _u32(prompt)
+        out = np.zeros((self.B, steps), np.uint32)
+        self.hip.gpu_decoder_generate_sampled(self.d, prompt.ravel(), prompt.shape[-1], steps, rngs, temperature, out)
         return out
 
     def destroy(self):
