@@ -488,7 +488,8 @@ def counter_probe(trlm, phase):
               two training steps (forward, CE, backward, AdamW) and one
               forward;
       decode: config 5's step kernels at context ~1000 -- a 1000-token
-              prefill of 64 sequences and 4 eager decode steps."""
+              prefill of 64 sequences and 4 eager decode steps, greedy,
+              then the same sampled at temperature 0.85."""
     host, hip = trlm.libs()
     rt = C.CDLL("libamdhip64.so")
     rt.hipMemcpyDtoD.argtypes = [C.c_void_p, C.c_void_p, C.c_size_t]
@@ -527,6 +528,8 @@ def counter_probe(trlm, phase):
             try:
                 prompt = rng.integers(0, V, DEC_B * 1000, dtype=np.uint32).reshape(DEC_B, 1000)
                 dec.generate_greedy(prompt, 5)
+                rngs = (trlm.PCGState * DEC_B)(*[host.pcg_seed(4242, 7 + b) for b in range(DEC_B)])
+                dec.generate_sampled(prompt, 5, rngs, DEC_TEMP)
             finally:
                 dec.destroy()
                 tr.destroy()
@@ -616,7 +619,8 @@ def counter_summary(phase, trace_dir, busy_dir, fetch_dir, write_dir):
     for k, v in sorted(dur.items(), key=lambda kv: -sum(kv[1])):
         if k not in ctr or "copyBuffer" in k[0]:
             continue
-        if phase == "decode" and not (k[0].startswith("k_dec_") or k[0].startswith("k_argmax")):
+        if phase == "decode" and not (k[0].startswith("k_dec_") or k[0].startswith("k_argmax") or
+                                      k[0].startswith("k_sample")):
             continue
         c = {n: float(np.median(x)) for n, x in ctr[k].items()}
         avg = sum(v) / len(v) / 1e3

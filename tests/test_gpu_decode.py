@@ -244,7 +244,7 @@ def test_sample_exponentials_equal_m_expf(trlm, orc, temp):
         pz, pe = C.c_void_p(dz), C.c_void_p(de)
         cl, cv, ct = C.c_int32(ld), C.c_int32(V), C.c_float(temp)
         args = (C.c_void_p * 5)(C.addressof(pz), C.addressof(cl), C.addressof(cv), C.addressof(ct), C.addressof(pe))
-        hip.hip_launch(f_, 8, rows, 1, 1024, 1, 1, 0, args)
+        hip.hip_launch(f_, rows, 8, 1, 1024, 1, 1, 0, args)
         got = dev.download(de, (rows, ld))[:, :V]
     finally:
         dev.close()

@@ -419,7 +419,7 @@ static void sample_exp(TrlmDecoder* d, f32 temperature) {
     hipDeviceptr_t lg = d->logits, e = d->e;
     i32 ld = (i32)d->ldv, V = (i32)d->V;
     void* args[] = { &lg, &ld, &V, &temperature, &e };
-    hip_launch(d->k_sample_exp, DEC_SAMPLE_CHUNKS, d->B, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
+    hip_launch(d->k_sample_exp, d->B, DEC_SAMPLE_CHUNKS, 1, DEC_SAMPLE_THREADS, 1, 1, 0, args);
 }
 
 /* TRLM_SAMPLE_SEQUENTIAL=1: every row takes the kernel's sequential path

@@ -214,14 +214,16 @@ __device__ float sample_expf(float xf) {
 #define SAMPLE_CHUNKS 8
 
 // e[row][j] = m_expf((z_j - max_v) / temperature) for the columns of chunk
-// blockIdx.x of row blockIdx.y (each workgroup forms the row's max itself:
+// blockIdx.y of row blockIdx.x (each workgroup forms the row's max itself:
 // the value of a max does not depend on the order, for rows without NaN).
+// Workgroup i goes to XCD i % 8, so with the row as the x index (64 rows, a
+// multiple of 8) a row's chunks share one XCD's L2 for those reads.
 extern "C" __global__ void __launch_bounds__(SAMPLE_THREADS)
 k_sample_exp(const float* __restrict__ logits, int ld, int V, float temperature, float* __restrict__ e) {
     // e rows have the logits' stride ld (a multiple of 4), for 16-byte reads
     constexpr int NW = SAMPLE_THREADS / 64;
     __shared__ float red[NW];
-    const int row = blockIdx.y, t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int row = blockIdx.x, t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const float* z = logits + (long long)row * ld;
     float mx = -INFINITY;
     // float4 reads, 8 in flight per thread (clamped addresses, masked after)
@@ -245,13 +247,16 @@ k_sample_exp(const float* __restrict__ logits, int ld, int V, float temperature,
 #pragma unroll
     for (int w = 1; w < NW; w++) mx = fmaxf(mx, red[w]);
     const int cw = (V + SAMPLE_CHUNKS - 1) / SAMPLE_CHUNKS;
-    const int c0 = blockIdx.x * cw, c1 = min(c0 + cw, V);
+    const int c0 = blockIdx.y * cw, c1 = min(c0 + cw, V);
     float* er = e + (long long)row * ld;
     for (int j = c0 + t; j < c1; j += SAMPLE_THREADS) er[j] = sample_expf((z[j] - mx) / temperature);
 }
 
 // The pick of one row from its e (block-wide; every thread returns it).
-__device__ int sample_row(int V, double u, const float* __restrict__ er, double* __restrict__ pr, int fallback_all) {
+// (inlined: as a called function it would need a stack, i.e. scratch memory
+// that the runtime sets up on the kernel's first launch)
+__device__ __forceinline__ int sample_row(int V, double u, const float* __restrict__ er, double* __restrict__ pr,
+                                          int fallback_all) {
 #pragma clang fp contract(off)
     constexpr int NW = SAMPLE_THREADS / 64;
     __shared__ double wsum[NW];
