@@ -62,6 +62,9 @@ def ref64(A, B, alpha=1.0, beta=0.0, C0=None, bias=None, resid=None):
     return r
 
 
+TILES = ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
+
+
 def close(got, want, tol=1e-4):
     scale = max(np.abs(want).max(), 1e-30)
     err = np.abs(got.astype(np.float64) - want).max()
@@ -184,6 +187,39 @@ def test_gemm_small_integers_exact(dev):
     for ta, tb in [(0, 0), (0, 1), (1, 0)]:
         got, _ = run_gemm(dev, A, B, ta, tb)
         assert np.array_equal(got, (A.astype(np.float64) @ B).astype(np.float32))
+
+
+@pytest.mark.parametrize("tile", TILES)
+@pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
+def test_gemm_epilogue_terms_bitwise(dev, tile, ta, tb):
+    """Each epilogue term alone and bias with the residual, on every forced
+    tile variant and split count, off-grid (edge tiles in M and N): with the
+    accumulation fixed by the forced plan, C must equal, bit for bit, the
+    plain product P = alpha*acc plus the term in fp32 (P + bias, resid + P,
+    P + C0 at beta 1, resid + (P + bias)).  The aligned operands take the
+    transposed LDS store, so this pins its row / column / term wiring; P
+    itself is checked against fp64."""
+    rng = np.random.default_rng(11 + len(tile) + 3 * ta + 7 * tb)
+    M, N, K = 300, 260, 1000
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, N)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = rng.standard_normal((M, N)).astype(np.float32)
+    try:
+        for splits in (1, 3):
+            dev.force(tile, splits)
+            P, var = run_gemm(dev, A, B, ta, tb, alpha=0.5)
+            assert var == ("k_gemm_%s_%s" % (["nn", "nt", "tn"][ta * 2 + tb], tile), splits), var
+            ok, rel = close(P, ref64(A, B, 0.5))
+            assert ok, (var, rel)
+            cases = [(dict(bias=bias), P + bias), (dict(resid=resid), resid + P),
+                     (dict(beta=1.0, C0=C0), P + C0), (dict(bias=bias, resid=resid), resid + (P + bias))]
+            for kw, want in cases:
+                got, _ = run_gemm(dev, A, B, ta, tb, alpha=0.5, **kw)
+                assert np.array_equal(got.view(np.uint32), want.astype(np.float32).view(np.uint32)), (var, sorted(kw))
+    finally:
+        dev.force(None)
 
 
 @pytest.mark.parametrize("ta,tb", [(0, 0), (0, 1), (1, 0)])
@@ -322,8 +358,6 @@ def test_gemm_lm_head_backward_rows(dev):
     print("lm_head_dw %s split %d: %.2e" % (var_w[0], var_w[1], rel))
     assert ok, (var_w, rel)
 
-
-TILES = ["256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
 
 
 @pytest.mark.parametrize("tile", TILES)

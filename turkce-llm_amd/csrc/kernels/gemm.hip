@@ -31,6 +31,13 @@
 //  - Tiles are visited XCD-aware: consecutive workgroups land on different
 //    XCDs, so the tile index is remapped so that each XCD works on a
 //    contiguous, M-grouped range of tiles and reuses operands in its own L2.
+//  - Results leave through LDS where the operand tiles' LDS can hold them:
+//    a wave's accumulators are written there 32 rows at a time and read back
+//    as whole row segments, so each wave-wide store covers 4-8 rows of
+//    128-256 bytes instead of 32 rows x 32 bytes.  The CU's vector-memory
+//    path is the contended resource of these kernels (a store straight from
+//    the accumulators waited ~0.5 us to issue), so fewer, fuller cache-line
+//    transactions per store are what the epilogue is tuned for.
 #include "common.h"
 
 #include <type_traits>
@@ -371,9 +378,112 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
 // stores (the compiler cannot move a load above a store that may alias it,
 // so interleaving them would expose every load's latency).  Everything else
 // takes the per-element path.
-template <int BM, int BN>
+//
+// Where the wave blocks fit in the workgroup's operand LDS (free once the
+// main loop's last barrier has passed) and the operands are 16-byte aligned,
+// the values go out through LDS instead (gemm_store_lds): a store straight
+// from the accumulators covers 32 rows x 32 bytes, one piece of 32 different
+// cache lines, while the transposed store covers whole row segments of the
+// wave's block.  The arithmetic per element is the same in both paths.
+template <int BM, int BN, bool PLAIN>
+__device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, const f32x16 (&acc)[BM / 64][BN / 64],
+                                               int r0, int c0, int lane, float* lw) {
+    constexpr int FM = BM / 64, FN = BN / 64;
+    constexpr int W = FN * 32;         // floats per row of the wave's block
+    constexpr int CPR = W / 4;         // 16-byte chunks per row (8 or 16)
+    constexpr int RPI = 64 / CPR;      // rows per wave-wide store (8 or 4)
+    const int half = lane >> 5, ml = lane & 31;
+    const int ch = lane % CPR, n = c0 + 4 * ch;
+    const bool full = n + 3 < p.N;
+    const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
+    const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;
+    f32x4 bv = {0.f, 0.f, 0.f, 0.f};
+    if (p.bias) {
+#pragma unroll
+        for (int q = 0; q < 4; q++) bv[q] = n + q < p.N ? p.bias[n + q] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < FM; i++) {
+        // 32 rows of the block: lane (ml, half) holds row ml, 16-byte chunks
+        // 8j + 2g + half; chunk k of row r sits at chunk k ^ (r % 8), so the
+        // 8 lanes an LDS cycle serves hit distinct banks on both sides
+#pragma unroll
+        for (int j = 0; j < FN; j++)
+#pragma unroll
+            for (int g = 0; g < 4; g++) {
+                f32x4 v;
+#pragma unroll
+                for (int q = 0; q < 4; q++) v[q] = p.alpha * acc[i][j][4 * g + q];
+                *(f32x4*)(lw + ml * W + 4 * ((8 * j + 2 * g + half) ^ (ml & 7))) = v;
+            }
+        __builtin_amdgcn_wave_barrier();   // one wave's LDS accesses complete in order
+        if constexpr (PLAIN) {
+#pragma unroll
+            for (int it = 0; it < 32 / RPI; it++) {
+                const int rr = it * RPI + lane / CPR;
+                const int row = r0 + i * 32 + rr;
+                const f32x4 v = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
+                float* dst = C + (long long)row * p.ldc + n;
+                if (row < p.M) {
+                    if (full) *(f32x4*)dst = v;
+                    else {
+#pragma unroll
+                        for (int q = 0; q < 4; q++)
+                            if (n + q < p.N) dst[q] = v[q];
+                    }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            continue;
+        }
+#pragma unroll
+        for (int it0 = 0; it0 < 32 / RPI; it0 += 4) {
+            f32x4 av[4];
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int row = r0 + i * 32 + (it0 + u) * RPI + lane / CPR;
+                av[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                if (addp && row < p.M) {
+                    const float* ap = addp + (long long)row * ldadd + n;
+                    if (full) av[u] = *(const f32x4*)ap;
+                    else {
+#pragma unroll
+                        for (int q = 0; q < 4; q++) av[u][q] = n + q < p.N ? ap[q] : 0.f;
+                    }
+                }
+            }
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const int rr = (it0 + u) * RPI + lane / CPR;
+                const int row = r0 + i * 32 + rr;
+                const f32x4 a = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
+                if (row >= p.M) continue;
+                f32x4 v;
+#pragma unroll
+                for (int q = 0; q < 4; q++) {
+                    float x = a[q];
+                    if (p.beta != 0.f) x = x + p.beta * av[u][q];
+                    if (p.bias) x = x + bv[q];
+                    if (p.resid) x = av[u][q] + x;
+                    v[q] = x;
+                }
+                if (p.rope_cos && n < p.rope_cols) rope4(p, row, n, v);
+                float* dst = C + (long long)row * p.ldc + n;
+                if (full) *(f32x4*)dst = v;
+                else {
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (n + q < p.N) dst[q] = v[q];
+                }
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   // this pass's reads before the next pass's writes
+    }
+}
+
+template <int BM, int BN, bool LDS_STORE = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, const f32x16 (&acc)[BM / 64][BN / 64],
-                                              int r0, int c0, int lane) {
+                                              int r0, int c0, int lane, float* lw = nullptr) {
     constexpr int FM = BM / 64, FN = BN / 64;
     constexpr int JG = FN < 2 ? FN : 2;
     const int half = lane >> 5, ml = lane & 31;
@@ -436,10 +546,23 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
     }
     const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
     const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;
-    const bool vec = !(p.beta != 0.f && p.resid) &&
-                     ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(p.resid) |
-                       reinterpret_cast<uintptr_t>(p.bias)) & 15) == 0 &&
-                     ((p.ldc | (p.resid ? p.ldr : 0)) & 3) == 0 && c0 + BN / 2 <= p.N;
+    const bool aligned = !(p.beta != 0.f && p.resid) &&
+                         ((reinterpret_cast<uintptr_t>(C) | reinterpret_cast<uintptr_t>(p.resid) |
+                           reinterpret_cast<uintptr_t>(p.bias)) & 15) == 0 &&
+                         ((p.ldc | (p.resid ? p.ldr : 0)) & 3) == 0;
+    if constexpr (LDS_STORE) {
+        if (aligned) {   // the same for every wave of the workgroup
+            __syncthreads();   // the main loop's LDS tiles (and column sums) are read
+            // alpha only (the LM head, the split-K partials): a store loop with
+            // no per-element selects
+            if (p.beta == 0.f && !p.bias && !p.resid && !p.rope_cos)
+                gemm_store_lds<BM, BN, true>(p, C, acc, r0, c0, lane, lw);
+            else
+                gemm_store_lds<BM, BN, false>(p, C, acc, r0, c0, lane, lw);
+            return;
+        }
+    }
+    const bool vec = aligned && c0 + BN / 2 <= p.N;
     if (vec) {
 #pragma unroll
         for (int i = 0; i < FM; i++) {
@@ -737,7 +860,9 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
         static_assert(BM == 64 && BN == 64 && PF == 2 && ALIGNED, "SwiGLU epilogue: 64x64 pipelined tiles");
         gemm_epilogue_glu(p, acc[0][0], m0 + wm0, tn, wave >> 1, wave & 1, lane, lds);
     } else {
-        gemm_epilogue<BM, BN>(p, C, acc, m0 + wm0, n0 + wn0, lane);
+        // the transposed store needs 32 rows of every wave's block in the operand LDS
+        constexpr bool LDS_STORE = 4 * 32 * (BN / 2) <= 2 * (ASZ + BSZ);
+        gemm_epilogue<BM, BN, LDS_STORE>(p, C, acc, m0 + wm0, n0 + wn0, lane, lds + wave * 32 * (BN / 2));
     }
 }
 
