@@ -522,8 +522,12 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
                 dvv[d][r] = dvv[d][r] + xch[(DB * 16 + d * 16 + r) * 64 + lane];
             }
         float* row = p.out + (rowbase + kpos) * p.ldq;
-        att_store_rows<HD>(row + kcol, dk, half, 1.0f, p.rope_cos, p.rope_sin, kpos);
-        att_store_rows<HD>(row + vcol, dvv, half, 1.0f);
+        // the lane's half taken afresh from mbcnt (lane id against an
+        // all-ones mask, whatever exec is): kept from the start, it was the
+        // one value the 256-register budget spilled across the loop
+        const int lh = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 5);
+        att_store_rows<HD>(row + kcol, dk, lh, 1.0f, p.rope_cos, p.rope_sin, kpos);
+        att_store_rows<HD>(row + vcol, dvv, lh, 1.0f);
     }
 }
 
