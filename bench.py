@@ -564,6 +564,8 @@ def gemm_roles():
             for rows in (m, m + 1):   # the weight gradients' partials carry the bias sums in an extra row
                 g2 = -(-(rows * n) // 256) * 256
                 roles.setdefault(("k_gemm_splitk_reduce", str(g2)), []).append(role + " reduce")
+                g4 = -(-(rows * n // 4) // 256) * 256   # four columns per thread (aligned operands)
+                roles.setdefault(("k_gemm_splitk_reduce4", str(g4)), []).append(role + " reduce")
     attn_grid = B * H * -(-T // 64) * 256
     for k in ("k_attn_fwd_hd64", "k_attn_bwd_dkv_hd64", "k_attn_bwd_dq_hd64"):
         roles[(k, str(attn_grid))] = ["B8 T1024"]

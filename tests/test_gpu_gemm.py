@@ -382,3 +382,53 @@ def test_gemm_every_tile_variant(dev, tile, ta, tb):
             assert ok, (var, rel)
     finally:
         dev.force(None)
+
+
+@pytest.mark.parametrize("splits", [1, 2, 5, 8, 13])
+def test_splitk_reduce4_equals_scalar_reduce(trlm, dev, splits):
+    """k_gemm_splitk_reduce4 (four columns per thread, taken when every operand
+    is 16-byte aligned) against k_gemm_splitk_reduce on the same partials:
+    same bits for every epilogue term and for the column-sum row (row M of
+    the partials), with split counts on both sides of its 4-wide load loop."""
+    import ctypes as C
+    _, hip = trlm.libs()
+    rng = np.random.default_rng(splits)
+    M, N, ldc, ldr = 37, 388, 392, 396
+    rows = M + 1
+    W = rng.standard_normal((splits, rows, N)).astype(np.float32)
+    C0 = rng.standard_normal((M, ldc)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+    resid = rng.standard_normal((M, ldr)).astype(np.float32)
+    dW, dbias, dres = dev.upload(W), dev.upload(bias), dev.upload(resid)
+    fs = hip.hip_get_kernel(C.byref(dev.ctx), b"k_gemm_splitk_reduce")
+    f4 = hip.hip_get_kernel(C.byref(dev.ctx), b"k_gemm_splitk_reduce4")
+    try:
+        for alpha, beta, use_b, use_r in [(1.0, 0.0, False, False), (0.5, 0.0, True, False), (0.5, 0.0, False, True),
+                                          (0.5, 1.0, True, False), (0.75, 0.0, True, True)]:
+            outs = []
+            for f, nthreads in ((fs, rows * N), (f4, rows * N // 4)):
+                dC, dcs = dev.upload(C0), dev.empty(N * 4)
+                a = [C.c_void_p(dW), C.c_int32(splits), C.c_int64(rows * N), C.c_void_p(dC), C.c_int32(M),
+                     C.c_int32(N), C.c_int32(ldc), C.c_float(alpha), C.c_float(beta),
+                     C.c_void_p(dbias if use_b else None), C.c_void_p(dres if use_r else None), C.c_int32(ldr),
+                     C.c_void_p(dcs)]
+                args = (C.c_void_p * len(a))(*[C.addressof(x) for x in a])
+                hip.hip_launch(f, (nthreads + 255) // 256, 1, 1, 256, 1, 1, 0, args)
+                outs.append((dev.download(dC, (M, ldc)), dev.download(dcs, N)))
+                dev.free(dC)
+                dev.free(dcs)
+            (cs, ss), (c4, s4) = outs
+            assert np.array_equal(cs.view(np.uint32), c4.view(np.uint32)), (alpha, beta, use_b, use_r)
+            assert np.array_equal(ss.view(np.uint32), s4.view(np.uint32))
+            want = alpha * W[:, :M, :].astype(np.float64).sum(0)
+            if beta:
+                want = want + beta * C0[:, :N]
+            if use_b:
+                want = want + bias
+            if use_r:
+                want = resid[:, :N] + want
+            assert np.abs(c4[:, :N] - want).max() <= 1e-5 * max(1.0, np.abs(want).max())
+            assert np.array_equal(c4[:, N:], C0[:, N:])   # columns past N untouched
+    finally:
+        for p in (dW, dbias, dres):
+            dev.free(p)

@@ -927,6 +927,49 @@ k_gemm_splitk_reduce(const float* __restrict__ W, int splits, long long sW, floa
     *dst = v;
 }
 
+// The same reduction four consecutive columns per thread (host: N, ldc, ldr
+// multiples of 4 and every pointer 16-byte aligned): 16-byte loads of every
+// split, the splits' loads issued four at a time ahead of their additions,
+// each column's sum still taken in split order and its epilogue in the
+// scalar kernel's order, so the results are the same bits.
+extern "C" __global__ void __launch_bounds__(256)
+k_gemm_splitk_reduce4(const float* __restrict__ W, int splits, long long sW, float* __restrict__ C, int M, int N,
+                      int ldc, float alpha, float beta, const float* __restrict__ bias,
+                      const float* __restrict__ resid, int ldr, float* __restrict__ csum) {
+    const long long i = 4 * ((long long)blockIdx.x * blockDim.x + threadIdx.x);
+    const long long rows = M + (csum ? 1 : 0);
+    if (i >= rows * N) return;
+    const int m = (int)(i / N), n = (int)(i - (long long)m * N);
+    f32x4 s = *(const f32x4*)(W + i);
+    int k = 1;
+    for (; k + 4 <= splits; k += 4) {
+        f32x4 w[4];
+#pragma unroll
+        for (int u = 0; u < 4; u++) w[u] = *(const f32x4*)(W + (long long)(k + u) * sW + i);
+#pragma unroll
+        for (int u = 0; u < 4; u++) s += w[u];
+    }
+    for (; k < splits; k++) s += *(const f32x4*)(W + (long long)k * sW + i);
+    if (m == M) {
+        *(f32x4*)(csum + n) = s;
+        return;
+    }
+    float* dst = C + (long long)m * ldc + n;
+    const f32x4 c = beta != 0.f ? *(const f32x4*)dst : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 b = bias ? *(const f32x4*)(bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+    const f32x4 r = resid ? *(const f32x4*)(resid + (long long)m * ldr + n) : f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4 o;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        float v = alpha * s[q];
+        if (beta != 0.f) v = v + beta * c[q];
+        if (bias) v = v + b[q];
+        if (resid) v = r[q] + v;
+        o[q] = v;
+    }
+    *(f32x4*)dst = o;
+}
+
 // Writes the raw accumulator of one MFMA whose A and B operands are the
 // lane's own values, so a host test can confirm the operand/result lane
 // layout the GEMMs assume.  out: [64 lanes][16 registers].

@@ -45,6 +45,7 @@ struct TrlmGemm {
     hipFunction_t k[3][T_COUNT];
     hipFunction_t ku[4];
     hipFunction_t reduce;
+    hipFunction_t reduce4;   /* four columns per thread, for 16-byte aligned operands */
     hipFunction_t glu;   /* k_gemm_nn_64x64_k32_glu */
     hipDeviceptr_t ws;
     u64 ws_floats;
@@ -69,6 +70,7 @@ TrlmGemm* trlm_gemm_create(HipCtx* ctx) {
         e->ku[l] = hip_get_kernel(ctx, name);
     }
     e->reduce = hip_get_kernel(ctx, "k_gemm_splitk_reduce");
+    e->reduce4 = hip_get_kernel(ctx, "k_gemm_splitk_reduce4");
     e->glu = hip_get_kernel(ctx, "k_gemm_nn_64x64_k32_glu");
     trlm_noalloc_setup(ctx->device);
     return e;
@@ -382,7 +384,14 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
     i32 sp = splits;
     i64 sW = (i64)slab;
     void* args[] = { &W, &sp, &sW, &C, &M, &N, &ldc, &alpha, &beta, &bias, &resid, &ldr, &csum };
-    hip_launch(e->reduce, (u32)((total + 255) / 256), 1, 1, 256, 1, 1, 0, args);
+    /* four columns per thread when every row segment of four is 16-byte
+     * aligned in each operand: same per-element order, same bits */
+    const int vec4 = (N % 4) == 0 && (ldc % 4) == 0 && (!resid || (ldr % 4) == 0) &&
+                     (((uintptr_t)W | (uintptr_t)C | (uintptr_t)bias | (uintptr_t)resid | (uintptr_t)csum) & 15u) == 0;
+    if (vec4)
+        hip_launch(e->reduce4, (u32)((total / 4 + 255) / 256), 1, 1, 256, 1, 1, 0, args);
+    else
+        hip_launch(e->reduce, (u32)((total + 255) / 256), 1, 1, 256, 1, 1, 0, args);
     return 0;
 }
 
