@@ -27,7 +27,8 @@
 //    128-bit LDS read per 4 MFMA steps: lane l feeds k = kk+4*(l/32)+s at
 //    step s, a permutation of k that both operands share.  An MN-contiguous
 //    operand is kept MN-contiguous and read 32 consecutive floats per
-//    half-wave (conflict-free).
+//    half-wave (conflict-free), as 64-bit reads of two interleaved blocks
+//    where the wave block is two MFMA blocks wide (GemmIlv).
 //  - Tiles are visited XCD-aware: consecutive workgroups land on different
 //    XCDs, so the tile index is remapped so that each XCD works on a
 //    contiguous, M-grouped range of tiles and reuses operands in its own L2.
@@ -108,6 +109,22 @@ struct TileLds {
     static constexpr int SIZE = KMAJOR ? R * (BK == 16 ? BK : BK + 4) : BK * R;
 };
 
+// Interleaved fragments.  An MN-contiguous operand whose wave block is two
+// 32-wide MFMA blocks (64 rows of A or columns of B) is read with block b
+// taking rows rb0 + 2*(l%32) + b: one 64-bit LDS read per k-step then feeds
+// both blocks (4 reads per 8-k chunk instead of 8 32-bit ones; LM-head dX /
+// dW +2.7 / +3.5 %).  Each output element still sums its k in the same
+// order, so the results are the same bits.  Only where the results leave
+// through LDS (gemm_store_lds), which places every value at its real row
+// and column; the epilogue's other paths map rows and columns the same way.
+template <int TA, int TB, int BM, int BN, int BK>
+struct GemmIlv {
+    static constexpr int ASZ = TileLds<BM, BK, TA == 0>::SIZE, BSZ = TileLds<BN, BK, TB == 1>::SIZE;
+    static constexpr bool LDS_STORE = 4 * 32 * (BN / 2) <= 2 * (ASZ + BSZ);
+    static constexpr bool A = TA == 1 && BM == 128 && LDS_STORE;
+    static constexpr bool B = TB == 0 && BN == 128 && LDS_STORE;
+};
+
 // Load one operand tile (R rows of m/n, BK of k) from global memory into
 // registers.  KMAJOR: element (r, k) at base[r*ld + k]; else base[k*ld + r].
 template <int R, int BK, bool KMAJOR, bool ALIGNED>
@@ -177,6 +194,24 @@ __device__ __forceinline__ f32x4 fetch_frag(const float* lds, int rb, int kk, in
 #pragma unroll
         for (int s = 0; s < 4; s++) v[s] = lds[(kq + s) * R + row];
         return v;
+    }
+}
+
+template <int R, int BK, bool KMAJOR, int NF, bool ILV = false>
+__device__ __forceinline__ void fetch_frags(const float* lds, int rb0, int kk, int lane, f32x4 (&f)[NF]) {
+    if constexpr (ILV) {
+        static_assert(!KMAJOR && NF == 2, "interleaved fragments: MN-contiguous operand, two blocks");
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        const int kq = kk + 4 * (lane >> 5);
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+            const f32x2 v = *(const f32x2*)(lds + (kq + s) * R + rb0 + 2 * (lane & 31));
+            f[0][s] = v[0];
+            f[1][s] = v[1];
+        }
+    } else {
+#pragma unroll
+        for (int i = 0; i < NF; i++) f[i] = fetch_frag<R, BK, KMAJOR>(lds, rb0 + i * 32, kk, lane);
     }
 }
 
@@ -267,10 +302,8 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* 
 #pragma unroll
         for (int kk = 0; kk < BK; kk += 8) {
             f32x4 fa[FM], fb[FN];
-#pragma unroll
-            for (int i = 0; i < FM; i++) fa[i] = fetch_frag<BM, BK, AK>(la, wm0 + i * 32, kk, lane);
-#pragma unroll
-            for (int j = 0; j < FN; j++) fb[j] = fetch_frag<BN, BK, BK_>(lb, wn0 + j * 32, kk, lane);
+            fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(la, wm0, kk, lane, fa);
+            fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(lb, wn0, kk, lane, fb);
 #pragma unroll
             for (int s = 0; s < 4; s++)
 #pragma unroll
@@ -284,11 +317,6 @@ __device__ __forceinline__ void gemm_mainloop(const GemmParams& p, const float* 
     }
 }
 
-template <int R, int BK, bool KMAJOR, int NF>
-__device__ __forceinline__ void fetch_frags(const float* lds, int rb0, int kk, int lane, f32x4 (&f)[NF]) {
-#pragma unroll
-    for (int i = 0; i < NF; i++) f[i] = fetch_frag<R, BK, KMAJOR>(lds, rb0 + i * 32, kk, lane);
-}
 
 // Interior tiles (every load in bounds, k-range a whole number of BK steps):
 // fragments double-buffered per 8-k chunk, next tile stored before the last
@@ -325,8 +353,8 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
     }
     __syncthreads();
     f32x4 fa[2][FM], fb[2][FN];
-    fetch_frags<BM, BK, AK, FM>(lds, wm0, 0, lane, fa[0]);
-    fetch_frags<BN, BK, BK_, FN>(lds + ASZ, wn0, 0, lane, fb[0]);
+    fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(lds, wm0, 0, lane, fa[0]);
+    fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(lds + ASZ, wn0, 0, lane, fb[0]);
     for (int kt = 0; kt < nk; kt++) {
         const float* la = lds + (kt & 1) * (ASZ + BSZ);
         float* ln = lds + ((kt & 1) ^ 1) * (ASZ + BSZ);
@@ -334,8 +362,8 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
         for (int c = 0; c < NC; c++) {
             const int u = c & 1, v = u ^ 1;
             if (c + 1 < NC) {
-                fetch_frags<BM, BK, AK, FM>(la, wm0, (c + 1) * 8, lane, fa[v]);
-                fetch_frags<BN, BK, BK_, FN>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
+                fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(la, wm0, (c + 1) * 8, lane, fa[v]);
+                fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
             } else {
                 // Last chunk of this tile: its fragments are in registers, so
                 // the other buffer can take the next tile before the barrier.
@@ -346,8 +374,8 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
                 }
                 __syncthreads();
                 if (kt + 1 < nk) {
-                    fetch_frags<BM, BK, AK, FM>(ln, wm0, 0, lane, fa[v]);
-                    fetch_frags<BN, BK, BK_, FN>(ln + ASZ, wn0, 0, lane, fb[v]);
+                    fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(ln, wm0, 0, lane, fa[v]);
+                    fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(ln + ASZ, wn0, 0, lane, fb[v]);
                     if (kt + 2 < nk) {
                         sa.load(ra);
                         sb.load(rb);
@@ -385,7 +413,7 @@ __device__ __forceinline__ void gemm_mainloop_full(const GemmParams& p, const fl
 // from the accumulators covers 32 rows x 32 bytes, one piece of 32 different
 // cache lines, while the transposed store covers whole row segments of the
 // wave's block.  The arithmetic per element is the same in both paths.
-template <int BM, int BN, bool PLAIN>
+template <int BM, int BN, bool PLAIN, bool ILA, bool ILB>
 __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, const f32x16 (&acc)[BM / 64][BN / 64],
                                                int r0, int c0, int lane, float* lw) {
     constexpr int FM = BM / 64, FN = BN / 64;
@@ -406,22 +434,37 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
     for (int i = 0; i < FM; i++) {
         // 32 rows of the block: lane (ml, half) holds row ml, 16-byte chunks
         // 8j + 2g + half; chunk k of row r sits at chunk k ^ (r % 8), so the
-        // 8 lanes an LDS cycle serves hit distinct banks on both sides
+        // 8 lanes an LDS cycle serves hit distinct banks on both sides.
+        // Interleaved rows (ILA): this pass's row ml is row 2*ml + i of the
+        // wave block.  Interleaved columns (ILB): register q of blocks 0 / 1
+        // holds column 2*(8g + 4*half + q) + 0 / 1, so each 16-byte chunk
+        // takes two registers of each block.
+        if constexpr (ILB) {
 #pragma unroll
-        for (int j = 0; j < FN; j++)
+            for (int g = 0; g < 4; g++)
 #pragma unroll
-            for (int g = 0; g < 4; g++) {
-                f32x4 v;
+                for (int qp = 0; qp < 4; qp += 2) {
+                    const f32x4 v = {p.alpha * acc[i][0][4 * g + qp], p.alpha * acc[i][1][4 * g + qp],
+                                     p.alpha * acc[i][0][4 * g + qp + 1], p.alpha * acc[i][1][4 * g + qp + 1]};
+                    *(f32x4*)(lw + ml * W + 4 * ((4 * g + 2 * half + qp / 2) ^ (ml & 7))) = v;
+                }
+        } else {
 #pragma unroll
-                for (int q = 0; q < 4; q++) v[q] = p.alpha * acc[i][j][4 * g + q];
-                *(f32x4*)(lw + ml * W + 4 * ((8 * j + 2 * g + half) ^ (ml & 7))) = v;
-            }
+            for (int j = 0; j < FN; j++)
+#pragma unroll
+                for (int g = 0; g < 4; g++) {
+                    f32x4 v;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) v[q] = p.alpha * acc[i][j][4 * g + q];
+                    *(f32x4*)(lw + ml * W + 4 * ((8 * j + 2 * g + half) ^ (ml & 7))) = v;
+                }
+        }
         __builtin_amdgcn_wave_barrier();   // one wave's LDS accesses complete in order
         if constexpr (PLAIN) {
 #pragma unroll
             for (int it = 0; it < 32 / RPI; it++) {
                 const int rr = it * RPI + lane / CPR;
-                const int row = r0 + i * 32 + rr;
+                const int row = ILA ? r0 + 2 * rr + i : r0 + i * 32 + rr;
                 const f32x4 v = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
                 float* dst = C + (long long)row * p.ldc + n;
                 if (row < p.M) {
@@ -441,7 +484,8 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
             f32x4 av[4];
 #pragma unroll
             for (int u = 0; u < 4; u++) {
-                const int row = r0 + i * 32 + (it0 + u) * RPI + lane / CPR;
+                const int rl = (it0 + u) * RPI + lane / CPR;
+                const int row = ILA ? r0 + 2 * rl + i : r0 + i * 32 + rl;
                 av[u] = f32x4{0.f, 0.f, 0.f, 0.f};
                 if (addp && row < p.M) {
                     const float* ap = addp + (long long)row * ldadd + n;
@@ -455,7 +499,7 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
 #pragma unroll
             for (int u = 0; u < 4; u++) {
                 const int rr = (it0 + u) * RPI + lane / CPR;
-                const int row = r0 + i * 32 + rr;
+                const int row = ILA ? r0 + 2 * rr + i : r0 + i * 32 + rr;
                 const f32x4 a = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
                 if (row >= p.M) continue;
                 f32x4 v;
@@ -481,12 +525,18 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
     }
 }
 
-template <int BM, int BN, bool LDS_STORE = false>
+template <int BM, int BN, bool LDS_STORE = false, bool ILA = false, bool ILB = false>
 __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, const f32x16 (&acc)[BM / 64][BN / 64],
                                               int r0, int c0, int lane, float* lw = nullptr) {
     constexpr int FM = BM / 64, FN = BN / 64;
     constexpr int JG = FN < 2 ? FN : 2;
     const int half = lane >> 5, ml = lane & 31;
+    // the row of accumulator block i in this lane, and the column of its
+    // register 4g + q in block j (interleaved fragments: see GemmIlv)
+    auto row_of = [&](int i) { return ILA ? r0 + 2 * ml + i : r0 + i * 32 + ml; };
+    auto col_of = [&](int j, int g, int q) {
+        return ILB ? c0 + 2 * (8 * g + 4 * half + q) + j : c0 + j * 32 + 8 * g + 4 * half + q;
+    };
     if (p.stats) {
         // Row statistics for a softmax over the row (the LM head's
         // cross-entropy): per row, the max of this wave's BN/2 columns of
@@ -505,7 +555,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                 for (int g = 0; g < 4; g++)
 #pragma unroll
                     for (int q = 0; q < 4; q++)
-                        if (c0 + j * 32 + 8 * g + 4 * half + q < p.N) mx = fmaxf(mx, p.alpha * acc[i][j][4 * g + q]);
+                        if (col_of(j, g, q) < p.N) mx = fmaxf(mx, p.alpha * acc[i][j][4 * g + q]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
             float sm = 0.f;
             if (mx != -INFINITY) {
@@ -515,21 +565,35 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                     for (int g = 0; g < 4; g++)
 #pragma unroll
                         for (int q = 0; q < 4; q++)
-                            if (c0 + j * 32 + 8 * g + 4 * half + q < p.N)
+                            if (col_of(j, g, q) < p.N)
                                 sm += __builtin_amdgcn_exp2f((p.alpha * acc[i][j][4 * g + q] - mx) * L2E);
             }
             sm += __shfl_xor(sm, 32, WAVE);
-            const int row = r0 + i * 32 + ml;
+            const int row = row_of(i);
             if (half == 0 && row < p.M) {
                 float* st = p.stats + 2 * ((long long)row * p.stats_ld + sc);
                 st[0] = mx;
                 st[1] = sm;
             }
             if (p.tgt && row < p.M) {
-                // the lane holding column t of this row (if the wave's columns
-                // include it) leaves that logit, the value C would hold
-                const int t = (int)p.tgt[row] - c0;
-                if (t >= 0 && t < BN / 2 && ((t >> 2) & 1) == half) {
+                // the lane holding the row's target column (if the wave's
+                // columns include it) leaves that logit, the value C would hold
+                const int tc = (int)p.tgt[row];
+                if constexpr (!ILA && !ILB) {
+                    const int t = tc - c0;
+                    if (t >= 0 && t < BN / 2 && ((t >> 2) & 1) == half) {
+                        float v = 0.f;
+#pragma unroll
+                        for (int j = 0; j < FN; j++)
+#pragma unroll
+                            for (int g = 0; g < 4; g++)
+#pragma unroll
+                                for (int q = 0; q < 4; q++)
+                                    if (t == j * 32 + 8 * g + 4 * half + q) v = p.alpha * acc[i][j][4 * g + q];
+                        p.tgt_val[row] = v;
+                    }
+                } else if (tc >= c0 && tc < c0 + BN / 2) {
+                    bool hit = false;
                     float v = 0.f;
 #pragma unroll
                     for (int j = 0; j < FN; j++)
@@ -537,8 +601,11 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                         for (int g = 0; g < 4; g++)
 #pragma unroll
                             for (int q = 0; q < 4; q++)
-                                if (t == j * 32 + 8 * g + 4 * half + q) v = p.alpha * acc[i][j][4 * g + q];
-                    p.tgt_val[row] = v;
+                                if (col_of(j, g, q) == tc) {
+                                    hit = true;
+                                    v = p.alpha * acc[i][j][4 * g + q];
+                                }
+                    if (hit) p.tgt_val[row] = v;
                 }
             }
         }
@@ -556,87 +623,139 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
             // alpha only (the LM head, the split-K partials): a store loop with
             // no per-element selects
             if (p.beta == 0.f && !p.bias && !p.resid && !p.rope_cos)
-                gemm_store_lds<BM, BN, true>(p, C, acc, r0, c0, lane, lw);
+                gemm_store_lds<BM, BN, true, ILA, ILB>(p, C, acc, r0, c0, lane, lw);
             else
-                gemm_store_lds<BM, BN, false>(p, C, acc, r0, c0, lane, lw);
+                gemm_store_lds<BM, BN, false, ILA, ILB>(p, C, acc, r0, c0, lane, lw);
             return;
         }
     }
-    const bool vec = aligned && c0 + BN / 2 <= p.N;
-    if (vec) {
+    if constexpr (!ILA && !ILB) {
+        const bool vec = aligned && c0 + BN / 2 <= p.N;
+        if (vec) {
+#pragma unroll
+            for (int i = 0; i < FM; i++) {
+                const int row = r0 + i * 32 + ml;
+                if (row >= p.M) continue;
+                float* crow = C + (long long)row * p.ldc;
+                const float* arow = addp + (long long)row * ldadd;
+#pragma unroll
+                for (int j0 = 0; j0 < FN; j0 += JG) {
+                    f32x4 av[JG][4], bv[JG][4];
+#pragma unroll
+                    for (int jj = 0; jj < JG; jj++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++) {
+                            const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
+                            const f32x4 z = {0.f, 0.f, 0.f, 0.f};
+                            av[jj][g] = addp ? *(const f32x4*)(arow + n) : z;
+                            bv[jj][g] = p.bias ? *(const f32x4*)(p.bias + n) : z;
+                        }
+#pragma unroll
+                    for (int jj = 0; jj < JG; jj++)
+#pragma unroll
+                        for (int g = 0; g < 4; g++) {
+                            f32x4 v;
+#pragma unroll
+                            for (int q = 0; q < 4; q++) {
+                                float x = p.alpha * acc[i][j0 + jj][4 * g + q];
+                                if (p.beta != 0.f) x = x + p.beta * av[jj][g][q];
+                                if (p.bias) x = x + bv[jj][g][q];
+                                if (p.resid) x = av[jj][g][q] + x;
+                                v[q] = x;
+                            }
+                            const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
+                            if (p.rope_cos && n < p.rope_cols) rope4(p, row, n, v);
+                            *(f32x4*)(crow + n) = v;
+                        }
+                }
+            }
+            return;
+        }
+    }
+    if constexpr (!ILA && !ILB) {
 #pragma unroll
         for (int i = 0; i < FM; i++) {
             const int row = r0 + i * 32 + ml;
             if (row >= p.M) continue;
             float* crow = C + (long long)row * p.ldc;
-            const float* arow = addp + (long long)row * ldadd;
+            const float* rrow = p.resid + (long long)row * p.ldr;
 #pragma unroll
-            for (int j0 = 0; j0 < FN; j0 += JG) {
-                f32x4 av[JG][4], bv[JG][4];
+            for (int j = 0; j < FN; j++)
 #pragma unroll
-                for (int jj = 0; jj < JG; jj++)
+                for (int g = 0; g < 4; g++) {
+                    float cv[4], rv[4], bv[4];
 #pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
-                        const f32x4 z = {0.f, 0.f, 0.f, 0.f};
-                        av[jj][g] = addp ? *(const f32x4*)(arow + n) : z;
-                        bv[jj][g] = p.bias ? *(const f32x4*)(p.bias + n) : z;
+                    for (int q = 0; q < 4; q++) {
+                        const int n = c0 + j * 32 + 8 * g + 4 * half + q;
+                        const bool ok = n < p.N;
+                        cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
+                        rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
+                        bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
                     }
+                    f32x4 v;
 #pragma unroll
-                for (int jj = 0; jj < JG; jj++)
-#pragma unroll
-                    for (int g = 0; g < 4; g++) {
-                        f32x4 v;
-#pragma unroll
-                        for (int q = 0; q < 4; q++) {
-                            float x = p.alpha * acc[i][j0 + jj][4 * g + q];
-                            if (p.beta != 0.f) x = x + p.beta * av[jj][g][q];
-                            if (p.bias) x = x + bv[jj][g][q];
-                            if (p.resid) x = av[jj][g][q] + x;
-                            v[q] = x;
-                        }
-                        const int n = c0 + (j0 + jj) * 32 + 8 * g + 4 * half;
-                        if (p.rope_cos && n < p.rope_cols) rope4(p, row, n, v);
-                        *(f32x4*)(crow + n) = v;
+                    for (int q = 0; q < 4; q++) {
+                        float x = p.alpha * acc[i][j][4 * g + q];
+                        if (p.beta != 0.f) x = x + p.beta * cv[q];
+                        if (p.bias) x = x + bv[q];
+                        if (p.resid) x = rv[q] + x;
+                        v[q] = x;
                     }
-            }
+                    const int n0g = c0 + j * 32 + 8 * g + 4 * half;
+                    if (p.rope_cos && n0g < p.rope_cols) rope4(p, row, n0g, v);
+#pragma unroll
+                    for (int q = 0; q < 4; q++)
+                        if (n0g + q < p.N) crow[n0g + q] = v[q];
+                }
         }
         return;
     }
+    // per element, in groups of four consecutive columns: block j's
+    // registers 4g .. 4g+3, or (interleaved columns) registers 4g + qp and
+    // 4g + qp + 1 of both blocks
 #pragma unroll
     for (int i = 0; i < FM; i++) {
-        const int row = r0 + i * 32 + ml;
+        const int row = row_of(i);
         if (row >= p.M) continue;
         float* crow = C + (long long)row * p.ldc;
         const float* rrow = p.resid + (long long)row * p.ldr;
 #pragma unroll
-        for (int j = 0; j < FN; j++)
-#pragma unroll
-            for (int g = 0; g < 4; g++) {
-                float cv[4], rv[4], bv[4];
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    const int n = c0 + j * 32 + 8 * g + 4 * half + q;
-                    const bool ok = n < p.N;
-                    cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
-                    rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
-                    bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
-                }
-                f32x4 v;
-#pragma unroll
-                for (int q = 0; q < 4; q++) {
-                    float x = p.alpha * acc[i][j][4 * g + q];
-                    if (p.beta != 0.f) x = x + p.beta * cv[q];
-                    if (p.bias) x = x + bv[q];
-                    if (p.resid) x = rv[q] + x;
-                    v[q] = x;
-                }
-                const int n0g = c0 + j * 32 + 8 * g + 4 * half;
-                if (p.rope_cos && n0g < p.rope_cols) rope4(p, row, n0g, v);
-#pragma unroll
-                for (int q = 0; q < 4; q++)
-                    if (n0g + q < p.N) crow[n0g + q] = v[q];
+        for (int gi = 0; gi < 4 * FN; gi++) {
+            f32x4 a;
+            int n0g;
+            if constexpr (ILB) {
+                const int g = gi >> 1, qp = 2 * (gi & 1);
+                a = f32x4{acc[i][0][4 * g + qp], acc[i][1][4 * g + qp], acc[i][0][4 * g + qp + 1],
+                          acc[i][1][4 * g + qp + 1]};
+                n0g = c0 + 2 * (8 * g + 4 * half + qp);
+            } else {
+                const int j = gi >> 2, g = gi & 3;
+                a = f32x4{acc[i][j][4 * g], acc[i][j][4 * g + 1], acc[i][j][4 * g + 2], acc[i][j][4 * g + 3]};
+                n0g = c0 + j * 32 + 8 * g + 4 * half;
             }
+            float cv[4], rv[4], bv[4];
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const int n = n0g + q;
+                const bool ok = n < p.N;
+                cv[q] = (ok && p.beta != 0.f) ? crow[n] : 0.f;
+                rv[q] = (ok && p.resid) ? rrow[n] : 0.f;
+                bv[q] = (ok && p.bias) ? p.bias[n] : 0.f;
+            }
+            f32x4 v;
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                float x = p.alpha * a[q];
+                if (p.beta != 0.f) x = x + p.beta * cv[q];
+                if (p.bias) x = x + bv[q];
+                if (p.resid) x = rv[q] + x;
+                v[q] = x;
+            }
+            if (p.rope_cos && n0g < p.rope_cols) rope4(p, row, n0g, v);
+#pragma unroll
+            for (int q = 0; q < 4; q++)
+                if (n0g + q < p.N) crow[n0g + q] = v[q];
+        }
     }
 }
 
@@ -729,8 +848,8 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
     }
     __syncthreads();
     f32x4 fa[2][FM], fb[2][FN];
-    fetch_frags<BM, BK, AK, FM>(lds, wm0, 0, lane, fa[0]);
-    fetch_frags<BN, BK, BK_, FN>(lds + ASZ, wn0, 0, lane, fb[0]);
+    fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(lds, wm0, 0, lane, fa[0]);
+    fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(lds + ASZ, wn0, 0, lane, fb[0]);
     // one tile: kt is computed from LDS buffer S = kt & 1; tile kt + 1 sits in
     // register set S and goes to buffer S ^ 1; set S then takes tile kt + 3
     auto tile = [&](auto S_, int kt) {
@@ -741,8 +860,8 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
         for (int c = 0; c < NC; c++) {
             const int u = c & 1, v = u ^ 1;
             if (c + 1 < NC) {
-                fetch_frags<BM, BK, AK, FM>(la, wm0, (c + 1) * 8, lane, fa[v]);
-                fetch_frags<BN, BK, BK_, FN>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
+                fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(la, wm0, (c + 1) * 8, lane, fa[v]);
+                fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(la + ASZ, wn0, (c + 1) * 8, lane, fb[v]);
             } else {
                 if (kt + 1 < nk) {
                     store_tile<BM, BK, AK>(ln, ra[S]);
@@ -751,8 +870,8 @@ __device__ __forceinline__ void gemm_mainloop_pf2(const GemmParams& p, const flo
                 }
                 __syncthreads();
                 if (kt + 1 < nk) {
-                    fetch_frags<BM, BK, AK, FM>(ln, wm0, 0, lane, fa[v]);
-                    fetch_frags<BN, BK, BK_, FN>(ln + ASZ, wn0, 0, lane, fb[v]);
+                    fetch_frags<BM, BK, AK, FM, GemmIlv<TA, TB, BM, BN, BK>::A>(ln, wm0, 0, lane, fa[v]);
+                    fetch_frags<BN, BK, BK_, FN, GemmIlv<TA, TB, BM, BN, BK>::B>(ln + ASZ, wn0, 0, lane, fb[v]);
                     if (kt + 3 < nk) {
                         sa.load(ra[S]);
                         sb.load(rb[S]);
@@ -862,7 +981,10 @@ __device__ __forceinline__ void gemm_body(const GemmParams& p) {
     } else {
         // the transposed store needs 32 rows of every wave's block in the operand LDS
         constexpr bool LDS_STORE = 4 * 32 * (BN / 2) <= 2 * (ASZ + BSZ);
-        gemm_epilogue<BM, BN, LDS_STORE>(p, C, acc, m0 + wm0, n0 + wn0, lane, lds + wave * 32 * (BN / 2));
+        using Ilv = GemmIlv<TA, TB, BM, BN, BK>;
+        static_assert(Ilv::LDS_STORE == LDS_STORE, "one rule for the transposed store");
+        gemm_epilogue<BM, BN, LDS_STORE, Ilv::A, Ilv::B>(p, C, acc, m0 + wm0, n0 + wn0, lane,
+                                                         lds + wave * 32 * (BN / 2));
     }
 }
 
