@@ -432,3 +432,61 @@ def test_splitk_reduce4_equals_scalar_reduce(trlm, dev, splits):
     finally:
         for p in (dW, dbias, dres):
             dev.free(p)
+
+
+
+@pytest.mark.parametrize("tile", ["128x128", "128x128_k32", "256x128", "64x128_k32", "64x64_k32"])
+@pytest.mark.parametrize("ta,tb", [(0, 0), (1, 0), (0, 1)])
+def test_gemm_store_paths_agree(dev, tile, ta, tb):
+    """With the accumulation fixed by the forced plan, the epilogue's two
+    store paths give the same bits: ldc a multiple of 4 takes the store
+    through LDS, an odd ldc the per-element path (both map the interleaved
+    fragments' rows and columns, for the NN / TN kernels that use them),
+    with alpha alone, bias + residual, and beta * C.  Columns past N are not
+    touched."""
+    rng = np.random.default_rng(17 + len(tile) + 3 * ta + tb)
+    M, N, K = 300, 260, 200
+    A = rng.standard_normal((M, K)).astype(np.float32)
+    B = rng.standard_normal((K, N)).astype(np.float32)
+    As, Bs = stored(A, ta), stored(B, tb)
+    bias = rng.standard_normal(N).astype(np.float32)
+    dA, dB, db = dev.upload(As), dev.upload(Bs), dev.upload(bias)
+    try:
+        dev.force(tile, 1)
+        for terms in ("alpha", "bias_resid", "beta"):
+            outs = []
+            for ldc in (N, N + 3):
+                C0 = rng.standard_normal((M, ldc)).astype(np.float32) if not outs else outs_c0_pad(outs[0][1], ldc)
+                R0 = C0.copy()
+                dC, dR = dev.upload(C0), dev.upload(R0)
+                kw = {}
+                if terms == "bias_resid":
+                    kw = dict(bias=db, resid=dR, ldr=ldc)
+                elif terms == "beta":
+                    kw = dict(beta=1.0)
+                dev.matmul(ta, tb, dA, dB, dC, M, N, K, As.shape[1], Bs.shape[1], ldc, alpha=0.5, **kw)
+                assert dev.last_variant() == ("k_gemm_%s_%s" % (["nn", "nt", "tn"][ta * 2 + tb], tile), 1)
+                got = dev.download(dC, (M, ldc))
+                outs.append((got, C0))
+                dev.free(dC)
+                dev.free(dR)
+            (g0, c0), (g1, c1) = outs
+            assert np.array_equal(g0[:, :N].view(np.uint32), g1[:, :N].view(np.uint32)), terms
+            assert np.array_equal(g1[:, N:], c1[:, N:])
+            want = ref64(A, B, 0.5, 1.0 if terms == "beta" else 0.0, c0[:, :N],
+                         bias if terms == "bias_resid" else None, c0[:, :N] if terms == "bias_resid" else None)
+            ok, rel = close(g0[:, :N], want)
+            assert ok, (terms, rel)
+    finally:
+        dev.force(None)
+        for p in (dA, dB, db):
+            dev.free(p)
+
+
+def outs_c0_pad(c0, ldc):
+    """The first run's initial C (and residual) widened to ldc columns, so
+    both runs add the same values."""
+    out = np.zeros((c0.shape[0], ldc), np.float32)
+    out[:, :c0.shape[1]] = c0[:, :min(c0.shape[1], ldc)]
+    out[:, c0.shape[1]:] = 7.0
+    return out

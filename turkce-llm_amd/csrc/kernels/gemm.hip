@@ -531,12 +531,12 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
     constexpr int FM = BM / 64, FN = BN / 64;
     constexpr int JG = FN < 2 ? FN : 2;
     const int half = lane >> 5, ml = lane & 31;
-    // the row of accumulator block i in this lane, and the column of its
-    // register 4g + q in block j (interleaved fragments: see GemmIlv)
+    // the row of accumulator block i in this lane (interleaved fragments:
+    // see GemmIlv; their columns are mapped in the paths below)
     auto row_of = [&](int i) { return ILA ? r0 + 2 * ml + i : r0 + i * 32 + ml; };
-    auto col_of = [&](int j, int g, int q) {
-        return ILB ? c0 + 2 * (8 * g + 4 * half + q) + j : c0 + j * 32 + 8 * g + 4 * half + q;
-    };
+    // Row statistics: the NT layout only (the host refuses others), so never
+    // with interleaved fragments
+    if constexpr (!ILA && !ILB) {
     if (p.stats) {
         // Row statistics for a softmax over the row (the LM head's
         // cross-entropy): per row, the max of this wave's BN/2 columns of
@@ -555,7 +555,7 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                 for (int g = 0; g < 4; g++)
 #pragma unroll
                     for (int q = 0; q < 4; q++)
-                        if (col_of(j, g, q) < p.N) mx = fmaxf(mx, p.alpha * acc[i][j][4 * g + q]);
+                        if (c0 + j * 32 + 8 * g + 4 * half + q < p.N) mx = fmaxf(mx, p.alpha * acc[i][j][4 * g + q]);
             mx = fmaxf(mx, __shfl_xor(mx, 32, WAVE));
             float sm = 0.f;
             if (mx != -INFINITY) {
@@ -565,35 +565,21 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                     for (int g = 0; g < 4; g++)
 #pragma unroll
                         for (int q = 0; q < 4; q++)
-                            if (col_of(j, g, q) < p.N)
+                            if (c0 + j * 32 + 8 * g + 4 * half + q < p.N)
                                 sm += __builtin_amdgcn_exp2f((p.alpha * acc[i][j][4 * g + q] - mx) * L2E);
             }
             sm += __shfl_xor(sm, 32, WAVE);
-            const int row = row_of(i);
+            const int row = r0 + i * 32 + ml;
             if (half == 0 && row < p.M) {
                 float* st = p.stats + 2 * ((long long)row * p.stats_ld + sc);
                 st[0] = mx;
                 st[1] = sm;
             }
             if (p.tgt && row < p.M) {
-                // the lane holding the row's target column (if the wave's
-                // columns include it) leaves that logit, the value C would hold
-                const int tc = (int)p.tgt[row];
-                if constexpr (!ILA && !ILB) {
-                    const int t = tc - c0;
-                    if (t >= 0 && t < BN / 2 && ((t >> 2) & 1) == half) {
-                        float v = 0.f;
-#pragma unroll
-                        for (int j = 0; j < FN; j++)
-#pragma unroll
-                            for (int g = 0; g < 4; g++)
-#pragma unroll
-                                for (int q = 0; q < 4; q++)
-                                    if (t == j * 32 + 8 * g + 4 * half + q) v = p.alpha * acc[i][j][4 * g + q];
-                        p.tgt_val[row] = v;
-                    }
-                } else if (tc >= c0 && tc < c0 + BN / 2) {
-                    bool hit = false;
+                // the lane holding column t of this row (if the wave's columns
+                // include it) leaves that logit, the value C would hold
+                const int t = (int)p.tgt[row] - c0;
+                if (t >= 0 && t < BN / 2 && ((t >> 2) & 1) == half) {
                     float v = 0.f;
 #pragma unroll
                     for (int j = 0; j < FN; j++)
@@ -601,15 +587,13 @@ __device__ __forceinline__ void gemm_epilogue(const GemmParams& p, float* C, con
                         for (int g = 0; g < 4; g++)
 #pragma unroll
                             for (int q = 0; q < 4; q++)
-                                if (col_of(j, g, q) == tc) {
-                                    hit = true;
-                                    v = p.alpha * acc[i][j][4 * g + q];
-                                }
-                    if (hit) p.tgt_val[row] = v;
+                                if (t == j * 32 + 8 * g + 4 * half + q) v = p.alpha * acc[i][j][4 * g + q];
+                    p.tgt_val[row] = v;
                 }
             }
         }
         if (p.no_store) return;
+    }
     }
     const float* addp = p.beta != 0.f ? C : p.resid;   // the one operand read per element
     const int ldadd = p.beta != 0.f ? p.ldc : p.ldr;

@@ -253,8 +253,9 @@ i32 trlm_gemm_ws(TrlmGemm* e, i32 trans_a, i32 trans_b, hipDeviceptr_t A, hipDev
         fprintf(stderr, "[HIP ERROR] trlm_gemm: RoPE epilogue needs a single GEMM and head width a multiple of 4\n");
         _exit(1);
     }
-    if (stats && (batch != 1 || beta != 0.0f || bias || resid)) {
-        fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single GEMM with no beta, bias or residual\n");
+    if (stats && (batch != 1 || beta != 0.0f || bias || resid || trans_a || !trans_b)) {
+        fprintf(stderr, "[HIP ERROR] trlm_gemm: row statistics need a single NT GEMM (the LM head's) with no beta, "
+                        "bias or residual\n");
         _exit(1);
     }
     if (x && (x->tgt || x->tgt_val || x->no_store) && (!stats || (x->tgt == NULL) != (x->tgt_val == NULL))) {
