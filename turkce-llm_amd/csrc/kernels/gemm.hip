@@ -461,6 +461,24 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
         }
         __builtin_amdgcn_wave_barrier();   // one wave's LDS accesses complete in order
         if constexpr (PLAIN) {
+            if (r0 + 32 * FM <= p.M && c0 + W <= p.N) {
+                // the wave block lies wholly inside C: every row of the pass
+                // is read back before the first store, so the stores wait on
+                // the LDS once per pass rather than once per row
+                f32x4 v[32 / RPI];
+#pragma unroll
+                for (int it = 0; it < 32 / RPI; it++) {
+                    const int rr = it * RPI + lane / CPR;
+                    v[it] = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
+                }
+                const int rl = lane / CPR;
+                float* dst = C + (long long)(ILA ? r0 + 2 * rl + i : r0 + i * 32 + rl) * p.ldc + n;
+                constexpr int STEP = ILA ? 2 * RPI : RPI;   // rows between the pass's stores
+#pragma unroll
+                for (int it = 0; it < 32 / RPI; it++) *(f32x4*)(dst + (long long)(it * STEP) * p.ldc) = v[it];
+                __builtin_amdgcn_wave_barrier();
+                continue;
+            }
 #pragma unroll
             for (int it = 0; it < 32 / RPI; it++) {
                 const int rr = it * RPI + lane / CPR;
