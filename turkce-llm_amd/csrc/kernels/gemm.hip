@@ -49,16 +49,25 @@
 // 20-40): pairs (2k, 2k+1) of a head of rope_hd columns rotated by
 // (cos, sin)[t = row % rope_T, k]; the tables are [rope_T][rope_hd/2].
 // n is a multiple of 4, so k is even and each table pair is one 8-byte load.
-__device__ __forceinline__ void rope4(const GemmParams& p, int row, int n, f32x4& v) {
-    typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+// (cos, sin) of the two pairs of columns n..n+3 of row `row`
+__device__ __forceinline__ void rope_tab(const GemmParams& p, int row, int n, f32x2& cc, f32x2& ss) {
     const int t = row % p.rope_T, k = (n % p.rope_hd) >> 1, hh = p.rope_hd >> 1;
-    const f32x2 cc = *(const f32x2*)(p.rope_cos + t * hh + k), ss = *(const f32x2*)(p.rope_sin + t * hh + k);
+    cc = *(const f32x2*)(p.rope_cos + t * hh + k);
+    ss = *(const f32x2*)(p.rope_sin + t * hh + k);
+}
+__device__ __forceinline__ void rope_rot(f32x4& v, f32x2 cc, f32x2 ss) {
     const float c0 = cc[0], c1 = cc[1], s0 = ss[0], s1 = ss[1];
     const f32x4 a = v;
     v[0] = a[0] * c0 - a[1] * s0;
     v[1] = a[0] * s0 + a[1] * c0;
     v[2] = a[2] * c1 - a[3] * s1;
     v[3] = a[2] * s1 + a[3] * c1;
+}
+__device__ __forceinline__ void rope4(const GemmParams& p, int row, int n, f32x4& v) {
+    f32x2 cc, ss;
+    rope_tab(p, row, n, cc, ss);
+    rope_rot(v, cc, ss);
 }
 
 __device__ __forceinline__ void gemm_tile_coords(const GemmParams& p, int& tm, int& tn, int& split) {
@@ -492,6 +501,50 @@ __device__ __forceinline__ void gemm_store_lds(const GemmParams& p, float* C, co
                         for (int q = 0; q < 4; q++)
                             if (n + q < p.N) dst[q] = v[q];
                     }
+                }
+            }
+            __builtin_amdgcn_wave_barrier();
+            continue;
+        }
+        if (r0 + 32 * FM <= p.M && c0 + W <= p.N) {
+            // interior wave block: per group of four rows, every global load
+            // (addend rows, RoPE tables) and LDS read is issued before the
+            // first store, so no store waits behind the next row's loads
+            const bool rope = p.rope_cos && n < p.rope_cols;
+#pragma unroll
+            for (int it0 = 0; it0 < 32 / RPI; it0 += 4) {
+                f32x4 av[4], a[4];
+                f32x2 cc[4], ss[4];
+                int row[4];
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int rl = (it0 + u) * RPI + lane / CPR;
+                    row[u] = ILA ? r0 + 2 * rl + i : r0 + i * 32 + rl;
+                    av[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    if (addp) av[u] = *(const f32x4*)(addp + (long long)row[u] * ldadd + n);
+                }
+                if (rope) {
+#pragma unroll
+                    for (int u = 0; u < 4; u++) rope_tab(p, row[u], n, cc[u], ss[u]);
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    const int rr = (it0 + u) * RPI + lane / CPR;
+                    a[u] = *(const f32x4*)(lw + rr * W + 4 * (ch ^ (rr & 7)));
+                }
+#pragma unroll
+                for (int u = 0; u < 4; u++) {
+                    f32x4 v;
+#pragma unroll
+                    for (int q = 0; q < 4; q++) {
+                        float x = a[u][q];
+                        if (p.beta != 0.f) x = x + p.beta * av[u][q];
+                        if (p.bias) x = x + bv[q];
+                        if (p.resid) x = av[u][q] + x;
+                        v[q] = x;
+                    }
+                    if (rope) rope_rot(v, cc[u], ss[u]);
+                    *(f32x4*)(C + (long long)row[u] * p.ldc + n) = v;
                 }
             }
             __builtin_amdgcn_wave_barrier();
