@@ -826,15 +826,19 @@ __device__ __forceinline__ void gemm_epilogue_glu(const GemmParams& p, const f32
     const int half = lane >> 5, ml = lane & 31;
     const int row = r0 + ml;
     const int cb = (wn == 0 ? 0 : p.glu_F) + 32 * tn;
-    f32x4 v[4];
+    f32x4 v[4], b[4];
+    // the bias loads go out before the first store: a load issued after a
+    // store waits behind it (the memory counter is in order)
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+        b[g] = p.bias ? *(const f32x4*)(p.bias + cb + 8 * g + 4 * half) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int g = 0; g < 4; g++) {
         const int n = cb + 8 * g + 4 * half;
-        const f32x4 b = p.bias ? *(const f32x4*)(p.bias + n) : f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int q = 0; q < 4; q++) {
             float x = p.alpha * acc[4 * g + q];
-            if (p.bias) x = x + b[q];
+            if (p.bias) x = x + b[g][q];
             v[g][q] = x;
         }
         if (row < p.M) *(f32x4*)(p.C + (long long)row * p.ldc + n) = v[g];
