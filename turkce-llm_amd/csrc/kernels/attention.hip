@@ -373,12 +373,20 @@ __device__ void flash_fwd(const AttnParams& p) {
 // grid (B*H, ceil(T/64)).  Wave w: key group g = w&1 (32 keys), query
 // partition part = w>>1 (64-query blocks at or after the keys' block,
 // alternating).  S and dP are formed as [q x kv] (one key per lane), so the
-// P and dS registers feed dV^T += dO^T P and dK^T += Q^T dS directly.
+// P and dS registers feed dV^T += dO^T P and dK^T += Q^T dS directly.  A
+// stage's four Q / dO tiles go straight from global memory into LDS, all in
+// flight together: one memory round trip per stage where register staging
+// (room for one tile beside the K, V operands and four accumulators) took
+// four (B8 T1024 hd64: 138.3 -> 135.0 us, same bits).
+// LDS address space for global_load_lds destinations
+typedef __attribute__((address_space(3))) void att_lds_void;
 template <int HD>
 __device__ void flash_bwd_dkv(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
     constexpr int LD = HD + 4;
     constexpr int TILE = 2 * 64 * LD + 128;                 // Q, dO, L, D of one query block
+    constexpr int NCH = 64 * LD / 256;                       // 1 KB global_load_lds chunks per tile
+    static_assert((64 * LD) % 256 == 0, "tile chunks");
     __shared__ __attribute__((aligned(16))) float lds[2 * TILE];
 
     const int lane = threadIdx.x & 63, half = lane >> 5;
@@ -414,33 +422,38 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
     const float* Ls = Gs + 64 * LD;
     const float* Ds = Ls + 64;
     for (int it = 0; it < niter; it++) {
-        // Q, dO (+ L, D) of the stage's two query blocks, one tile at a time:
-        // a tile's loads are in flight together, then stored (the K, V
-        // operands and four accumulators leave room for one tile only).
-        // Unconditional: blocks past the end load clamped rows, store zeros.
+        // Q and dO of the stage's two query blocks go straight into LDS
+        // (global_load_lds: 1 KB per wave instruction, rows [64][LD], pad
+        // columns a copy of column 0 that is never read), all four tiles in
+        // flight together; rows past the end are clamped to the last row:
+        // their probabilities are masked to 0, so their products are 0.
+        // L and D go through registers.  Unconditional: blocks past the end
+        // load clamped rows and are skipped below.
+        __syncthreads();                                     // every wave is done with the last stage
 #pragma unroll
         for (int tt = 0; tt < 4; tt++) {
-            const int pp = tt >> 1, jp = 2 * it + pp;
+            const int pp = tt >> 1, q0 = (kb + 2 * it + pp) * 64;
             const bool isq = (tt & 1) == 0;
-            const int q0 = (kb + jp) * 64;
-            AttTile<HD> tl;
-            float lv = 0.f, dd = 0.f;
-            if (isq) tl.load(qkv, p.ldq, q0, p.T, qcol);
-            else tl.load(dO, p.ldo, q0, p.T, qcol);
-            const int q = q0 + (threadIdx.x & 63);
-            if (isq && threadIdx.x < 64) {
-                const int qc = q < p.T ? q : p.T - 1;
-                lv = lse[qc];
-                dd = dv[qc];
-            }
-            if (tt == 0) __syncthreads();
-            float* base = lds + pp * TILE;
-            tl.store(base + (isq ? 0 : 64 * LD), q0, p.T);
-            if (isq && threadIdx.x < 64) {
-                base[2 * 64 * LD + threadIdx.x] = q < p.T ? lv : 0.f;
-                base[2 * 64 * LD + 64 + threadIdx.x] = q < p.T ? dd : 0.f;
+            const float* src = isq ? qkv + qcol : dO + qcol;
+            const int ld = isq ? p.ldq : p.ldo;
+            float* dst = lds + pp * TILE + (isq ? 0 : 64 * LD);
+            for (int ci = wave; ci < NCH; ci += 4) {
+                const int pos = 256 * ci + 4 * lane;
+                const int r = pos / LD, col = pos - r * LD;
+                const int row = q0 + r < p.T ? q0 + r : p.T - 1;
+                __builtin_amdgcn_global_load_lds((const void*)(src + (long long)row * ld + (col < HD ? col : 0)),
+                                                 (att_lds_void*)(dst + 256 * ci), 16, 0, 0);
             }
         }
+        if (threadIdx.x < 128) {
+            const int pp = threadIdx.x >> 6, q = (kb + 2 * it + pp) * 64 + (threadIdx.x & 63);
+            const int qc = q < p.T ? q : p.T - 1;
+            const float lv = lse[qc], dd = dv[qc];
+            float* base = lds + pp * TILE + 2 * 64 * LD;
+            base[threadIdx.x & 63] = q < p.T ? lv : 0.f;
+            base[64 + (threadIdx.x & 63)] = q < p.T ? dd : 0.f;
+        }
+        __builtin_amdgcn_s_waitcnt(0);                       // this wave's tile chunks have landed
         __syncthreads();
         const int j = 2 * it + part;
         if (j >= nblk) continue;
@@ -522,12 +535,8 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
                 dvv[d][r] = dvv[d][r] + xch[(DB * 16 + d * 16 + r) * 64 + lane];
             }
         float* row = p.out + (rowbase + kpos) * p.ldq;
-        // the lane's half taken afresh from mbcnt (lane id against an
-        // all-ones mask, whatever exec is): kept from the start, it was the
-        // one value the 256-register budget spilled across the loop
-        const int lh = (int)(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) >> 5);
-        att_store_rows<HD>(row + kcol, dk, lh, 1.0f, p.rope_cos, p.rope_sin, kpos);
-        att_store_rows<HD>(row + vcol, dvv, lh, 1.0f);
+        att_store_rows<HD>(row + kcol, dk, half, 1.0f, p.rope_cos, p.rope_sin, kpos);
+        att_store_rows<HD>(row + vcol, dvv, half, 1.0f);
     }
 }
 
@@ -549,7 +558,6 @@ __device__ void flash_bwd_dkv(const AttnParams& p) {
 // workgroups fit a CU.  B8 T1024 hd64: 40.4 us against 49.5 for two key
 // blocks per stage with a transposed register-staged K tile (and 54.7 for
 // that form in plain longest-first order).
-typedef __attribute__((address_space(3))) void att_lds_void;
 template <int HD>
 __device__ void flash_bwd_dq_ds(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
