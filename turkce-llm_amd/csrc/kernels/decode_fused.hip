@@ -451,7 +451,7 @@ template <int HD, int SEQ, int WPS, int NIT = 4>
 __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
     constexpr int LPR = HD / 4, RPI = 64 / LPR;
     constexpr int TW = SEQ * WPS;               // waves of the workgroup
-    constexpr int GB = 4;                       // row groups per load batch of the projection
+    constexpr int GB = 12;                      // row groups per load batch of the projection
     __shared__ f32x4_t red[TW][SEQ][3][LPR];    // the waves' partial q | k | v sums
     __shared__ f32x4_t hv[SEQ][3][LPR];         // each sequence's q, new k, new v
     __shared__ float wm[TW], wl[TW];
@@ -542,6 +542,9 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
 #pragma unroll
             for (int g = 0; g < 3; g++) wv[j][g] = ld4(wcol + ks * p.ldw + g * D);
         }
+        // every load of the batch is issued before the first use (left to
+        // itself the scheduler keeps a few in flight and waits on each in turn)
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int j = 0; j < GB; j++) {
             const int i = g0 + j * RPI + sub;           // row offset inside the wave's range
@@ -637,7 +640,7 @@ __device__ __forceinline__ void dec_qkv_attn(const DecGemmParams& p) {
 #define DEC_QA_WPS 4
 #define DEC_QKV_ATTN_KERNEL(HD)                                                                         \
     extern "C" __global__ void __launch_bounds__(64 * DEC_QA_SEQ * DEC_QA_WPS)                           \
-        __attribute__((amdgpu_waves_per_eu(4))) k_dec_qkv_attn_hd##HD(DecGemmParams p) {               \
+        __attribute__((amdgpu_waves_per_eu(2))) k_dec_qkv_attn_hd##HD(DecGemmParams p) {               \
         dec_qkv_attn<HD, DEC_QA_SEQ, DEC_QA_WPS>(p);                                                    \
     }
 DEC_QKV_ATTN_KERNEL(16)
