@@ -90,22 +90,42 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
 
     // wave 0's epilogue inputs, loaded now so they arrive with the operands:
     // bias and residual rows (this lane's 4 rows per row block)
+    // No load sits under a per-element branch: a branch that joins after a
+    // load makes the join wait for it, which chained these loads one after
+    // another in front of the operand stream.
     float ebias[NACC], eres[RB][4];
     if (w == 0) {
+        // any valid address when there is no bias (the value is then not
+        // used: the epilogue selects 0, so nothing waits for it here)
+        const float* bsrc = p.bias ? p.bias : p.W;
 #pragma unroll
-        for (int a = 0; a < NACC; a++) ebias[a] = p.bias ? p.bias[bcol[a]] : 0.f;
+        for (int a = 0; a < NACC; a++) ebias[a] = bsrc[bcol[a]];
 #pragma unroll
         for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-            for (int r = 0; r < 4; r++) {
-                eres[rb][r] = 0.f;
-                if (MODE == DM_PLAIN && (p.resid || p.resid_ids)) {
-                    int m = m0 + 16 * rb + 4 * kq + r;
-                    if (m > p.M - 1) m = p.M - 1;
-                    eres[rb][r] = p.resid_ids ? p.E[(long long)p.ids[m] * p.ldr + bcol[0]]
-                                              : p.resid[(long long)m * p.ldr + bcol[0]];
+            for (int r = 0; r < 4; r++) eres[rb][r] = 0.f;
+        if (MODE == DM_PLAIN && p.resid_ids) {
+            unsigned id[RB][4];
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + 16 * rb + 4 * kq + r;
+                    id[rb][r] = p.ids[m < p.M ? m : p.M - 1];
                 }
-            }
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) eres[rb][r] = p.E[(long long)id[rb][r] * p.ldr + bcol[0]];
+        } else if (MODE == DM_PLAIN && p.resid) {
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const int m = m0 + 16 * rb + 4 * kq + r;
+                    eres[rb][r] = p.resid[(long long)(m < p.M ? m : p.M - 1) * p.ldr + bcol[0]];
+                }
+        }
     }
 
     f32x4_t acc[RB][NACC];
@@ -218,7 +238,7 @@ __device__ __forceinline__ void dec_gemm(const DecGemmParams& p) {
             const float scale = NORM ? rn[mrow] : 1.0f;
             float o[NACC];
 #pragma unroll
-            for (int a = 0; a < NACC; a++) o[a] = v[a][r] * scale + ebias[a];
+            for (int a = 0; a < NACC; a++) o[a] = v[a][r] * scale + (p.bias ? ebias[a] : 0.f);
             if (MODE == DM_SWIGLU) {
                 const float g = o[0], u = o[NACC - 1];
                 const float sg = 1.0f / (1.0f + expf(-g));
