@@ -281,18 +281,34 @@ __device__ __forceinline__ void dec_head(const DecGemmParams& p) {
     const int nwaves = gridDim.x * DEC_HEAD_WAVES;
 
     // this wave's rows w, w + 8, ... and the norm weight (clamped loads)
+    // (the row addresses are formed first, under one branch on a_ids: a
+    // per-row branch around the id load made every row wait for the rows
+    // before it)
     f32x4_t xv[RPW][2], nw[2];
+    const float* xr[RPW];
+    if (p.a_ids) {
+        unsigned id[RPW];
 #pragma unroll
-    for (int r = 0; r < RPW; r++) {
-        int m = m0 + w + DEC_HEAD_WAVES * r;
-        if (m > p.M - 1) m = p.M - 1;
-        const float* xr = p.a_ids ? p.E + (long long)p.ids[m] * p.lda : p.A + (long long)m * p.lda;
+        for (int r = 0; r < RPW; r++) {
+            const int m = m0 + w + DEC_HEAD_WAVES * r;
+            id[r] = p.ids[m < p.M ? m : p.M - 1];
+        }
+#pragma unroll
+        for (int r = 0; r < RPW; r++) xr[r] = p.E + (long long)id[r] * p.lda;
+    } else {
+#pragma unroll
+        for (int r = 0; r < RPW; r++) {
+            const int m = m0 + w + DEC_HEAD_WAVES * r;
+            xr[r] = p.A + (long long)(m < p.M ? m : p.M - 1) * p.lda;
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPW; r++)
 #pragma unroll
         for (int t = 0; t < 2; t++) {
             const int q = lane + 64 * t;
-            xv[r][t] = ld4(xr + 4 * (q < K4 ? q : 0));
+            xv[r][t] = ld4(xr[r] + 4 * (q < K4 ? q : 0));
         }
-    }
 #pragma unroll
     for (int t = 0; t < 2; t++) {
         const int q = lane + 64 * t;
