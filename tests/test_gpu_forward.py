@@ -48,7 +48,9 @@ def test_config1_logits_and_greedy(trlm, orc, real_model):
     print("config1: logits rel err %.3e, next token %d (oracle %d)" % (err, am[-1], ref_next[-1]))
 
 
-@pytest.mark.parametrize("V,D,H,L,F,T,B", [(50, 32, 2, 2, 48, 12, 5), (500, 64, 2, 2, 128, 256, 3)])
+@pytest.mark.parametrize("V,D,H,L,F,T,B", [(50, 32, 2, 2, 48, 12, 5), (500, 64, 2, 2, 128, 256, 3),
+                                           # config 3's B8 T1024 rows at the real width, every logit compared
+                                           (2000, 384, 6, 2, 1024, 1024, 8)])
 def test_forward_loss_keeps_logits(trlm, orc, V, D, H, L, F, T, B):
     model = orc.Model(V, D, H, L, F)
     params = model.init(1337, 1)

@@ -4,8 +4,9 @@ assertions of the reference's tests/test_gpu_train.c, at a 1e-4 bar.
 Cases (test_gpu_train.c:261-271): small shapes off every tile grid
 (V50 D32 H2 L2 F48 T12 B5), long context (V500 D64 H2 L2 F128 T1024 B2),
 and the real model (V31769 D384 H6 L12 F1024 T128 B4); plus ragged
-attention blocks and 320 attention workgroups (more than one dispatch
-round of 256).  Inputs exactly as
+attention blocks, 320 attention workgroups (more than one dispatch
+round of 256), and config 4's B8 T1024 activations at the real width with
+a 2000-word vocabulary (V2000 D384 H6 L2 F1024).  Inputs exactly as
 the reference test builds them: weights lm_init(pcg_seed(1337,1)), tokens
 pcg_range_i64(0, V-1) from pcg_seed(4242,7), batch seed 2026.
 
@@ -33,6 +34,12 @@ CASES = {
     # 320 attention workgroups (B*H*blocks): the attention forward's order
     # reverses its second dispatch round of 256, here a partial one (hd 64)
     "many_blocks": dict(V=200, D=128, H=2, L=1, F=96, T=640, B=16, ntok=20000),
+    # config 4's activations at full size (B8 T1024: M = 8192 rows, the real
+    # width D384 H6 F1024) with a 2000-word vocabulary and two layers, so
+    # that every gradient tensor is compared whole: the layer GEMMs take the
+    # benchmark's own tiles and split-K factors and the attention its
+    # 768-workgroup grid at head dim 64
+    "config4_width": dict(V=2000, D=384, H=6, L=2, F=1024, T=1024, B=8, ntok=40000),
 }
 TOL = 1e-4
 

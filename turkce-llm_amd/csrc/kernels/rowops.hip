@@ -488,11 +488,18 @@ k_cross_entropy(float* __restrict__ logits, int ld, const unsigned* __restrict__
     float M = sm[0], S = ss[0];
     for (int w = 1; w < 4; w++) ms_combine(M, S, sm[w], ss[w]);
     // zt_rows (with stats, no gradient): the LM-head GEMM left each row's
-    // target logit and never wrote the logits
-    unsigned t = targets[row];
-    float zt = zt_rows ? zt_rows[row] : z[t];
+    // target logit and never wrote the logits.  The loss is stored before
+    // the barrier: the target logit's load then has to complete before the
+    // other waves start overwriting the row with the gradient.  (With the
+    // store after the barrier, the compiler turned the uniform load into a
+    // scalar load and sank it below the barrier into thread 0's branch, so it
+    // could read the target's gradient instead of its logit.)
+    const unsigned t = targets[row];
+    if (threadIdx.x == 0) {
+        const float zt = zt_rows ? zt_rows[row] : z[t];
+        loss_rows[row] = (float)log((double)S) + M - zt;
+    }
     __syncthreads();
-    if (threadIdx.x == 0) loss_rows[row] = (float)log((double)S) + M - zt;
     if (!write_grad) return;
     float inv = 1.0f / S;
     if (vec) {
