@@ -18,7 +18,9 @@ slide) that last row is what the decoder must produce, so:
     generation on the device equals the per-token loop;
   - at the real architecture (V 31769, D 384, L 12) the decoder equals the
     GPU trainer's full forward (itself pinned to the oracle) at the last
-    position, within 1e-4.
+    position, within 1e-4; and at config 5's own shape (batch 64, 128-token
+    prompts, 8 teacher-forced steps) it equals the oracle's forward on four
+    of the sequences at every position, within 1e-4.
 """
 import numpy as np
 import pytest
@@ -285,6 +287,44 @@ def test_real_architecture_against_gpu_full_forward(trlm, orc):
                 dec.step(nxt)
                 ctx = np.concatenate([ctx, nxt[:, None]], axis=1)
         print("real-scale decode: last rel err %.2e" % err)
+    finally:
+        dec.destroy()
+        tr.destroy()
+        hm.close()
+
+
+def test_config5_shape_against_oracle(trlm, orc):
+    """Config 5's shape (the real model, batch 64, 128-token prompts) against
+    the oracle itself: 8 teacher-forced steps, so every step's context is
+    known in advance and one oracle forward over the whole 136 tokens gives
+    the reference logits of every position (attention is causal).  Four of
+    the 64 sequences are compared -- the two sequence pairs that share the
+    first and last attention workgroups -- after the prefill and after each
+    step, within 1e-4 of max|logits|; each greedy pick is the first maximum
+    of the decoder's own logits."""
+    V, D, H, L, F, B, P, S = 31769, 384, 6, 12, 1024, 64, 128, 8
+    sel = np.array([0, 1, 62, 63])
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    ctx = orc.random_tokens(B * (P + S), V, 4242, 9, hi_exclusive=V).reshape(B, P + S)
+    want = model.forward_logits(params, np.ascontiguousarray(ctx[sel]).ravel(), len(sel), P + S)
+    want = want.reshape(len(sel), P + S, V)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, 1, 8)
+    dec = trlm.Decoder(tr, B, P + S + 1)
+    try:
+        dec.prefill(np.ascontiguousarray(ctx[:, :P]))
+        worst = 0.0
+        for s in range(S + 1):
+            got = dec.logits()
+            assert dec.length() == P + s
+            err = rel_err(got[sel], want[:, P + s - 1, :])
+            worst = max(worst, err)
+            assert err <= 1e-4, (s, err)
+            assert np.array_equal(dec.greedy(), np.argmax(got, axis=1).astype(np.uint32))
+            if s < S:
+                dec.step(np.ascontiguousarray(ctx[:, P + s]))
+        print("config-5 shape against the oracle: worst rel err %.2e over %d positions" % (worst, S + 1))
     finally:
         dec.destroy()
         tr.destroy()
