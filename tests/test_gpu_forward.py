@@ -48,6 +48,31 @@ def test_config1_logits_and_greedy(trlm, orc, real_model):
     print("config1: logits rel err %.3e, next token %d (oracle %d)" % (err, am[-1], ref_next[-1]))
 
 
+@pytest.mark.parametrize("V", [700, 2000, 5003])
+def test_training_loss_equals_forward_loss(trlm, orc, V):
+    """The loss forward_backward returns equals the forward-only loss bit for
+    bit, five times in a row, at vocabularies where every wave of the
+    cross-entropy's row writes gradient values in its first pass (V > 1024
+    columns, and V % 4 != 0 for the per-element path): the row's target
+    logit must be read before any of them overwrites it."""
+    D, H, L, F, T, B = 32, 2, 1, 32, 64, 8
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    toks = orc.random_tokens(4000, V)
+    ids, tgt = orc.sample_batch(toks, T, B, 31)
+    hm = trlm.HostModel(V, D, H, L, F, params)
+    tr = trlm.Trainer(hm, B, T)
+    try:
+        want = np.float32(tr.forward_loss_logits(ids, tgt, want_logits=False)[0])
+        got = [np.float32(tr.forward_backward(ids, tgt)) for _ in range(5)]
+    finally:
+        tr.destroy()
+        hm.close()
+    cpu_loss, _, _ = model.forward_backward(params, ids, tgt, B, T, want_grads=False)
+    assert abs(float(want) - cpu_loss) <= 1e-4 * abs(cpu_loss)
+    assert all(g.view(np.uint32) == want.view(np.uint32) for g in got), (want, got)
+
+
 @pytest.mark.parametrize("V,D,H,L,F,T,B", [(50, 32, 2, 2, 48, 12, 5), (500, 64, 2, 2, 128, 256, 3),
                                            # config 3's B8 T1024 rows at the real width, every logit compared
                                            (2000, 384, 6, 2, 1024, 1024, 8)])
