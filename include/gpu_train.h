@@ -89,6 +89,8 @@ typedef struct GpuTrainer {
     hipDeviceptr_t ce_stats;                  /* [N][ce_stats_cap] (max, sum) from the LM-head GEMM */
     i32 ce_stats_cap, ce_nst;
     hipDeviceptr_t ce_zt;                     /* [N] each row's target logit (eval: logits not stored) */
+    hipDeviceptr_t attn_jobs;                 /* [B*H*ceil(T/64)] i32: the attention forward's job table */
+    hipDeviceptr_t attn_fwd_jobs;             /* attn_jobs when the table applies (trlm_attn_job_table), else 0 */
 } GpuTrainer;
 
 GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMModel* model,

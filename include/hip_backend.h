@@ -68,6 +68,13 @@ void hip_sync(void);                                          /* cuda_backend.h:
 /* The stream of the context current on this thread (for event timing). */
 hipStream_t hip_current_stream(void);
 
+/* Not in the reference's backend: the compute units of the current
+ * context's device, and how many workgroups of block_threads threads of
+ * kernel f one compute unit holds at once (the attention forward places its
+ * jobs by them). */
+u32 hip_cu_count(void);
+u32 hip_blocks_per_cu(hipFunction_t f, u32 block_threads);
+
 /* Overlap within one context (not in the reference's backend): a second
  * stream at default priority.  hip_side_begin() sends the current context's
  * later launches to it, ordered after everything already queued on the main

@@ -29,7 +29,7 @@ class AttnParams(C.Structure):
     _fields_ = [("qkv", C.c_void_p), ("out", C.c_void_p), ("O", C.c_void_p), ("dO", C.c_void_p),
                 ("lse", C.c_void_p), ("dvec", C.c_void_p), ("B", C.c_int), ("T", C.c_int), ("H", C.c_int),
                 ("D", C.c_int), ("ldq", C.c_int), ("ldo", C.c_int), ("scale", C.c_float),
-                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("ds", C.c_void_p)]
+                ("rope_cos", C.c_void_p), ("rope_sin", C.c_void_p), ("ds", C.c_void_p), ("jobs", C.c_void_p)]
 
 
 def _reference(qkv, dO, B, T, H, HD, cos, sin):
@@ -153,3 +153,42 @@ def test_attention_kernels_match_float64(trlm, case):
     _check("dK", grads[0][:, D:2 * D], want_d[:, D:2 * D], mag[:, D:2 * D])
     _check("dV", grads[0][:, 2 * D:], want_d[:, 2 * D:])
     assert np.array_equal(grads[0].view(np.uint32), grads[1].view(np.uint32))
+
+
+@pytest.mark.parametrize("B,H,T", [(8, 6, 1024), (2, 3, 200)])
+def test_forward_job_placement_keeps_bits(trlm, B, H, T):
+    """The forward's job placement (AttnParams.jobs) changes which workgroup
+    takes which (query block, head), never what it computes: O and the
+    log-sum-exp are the same bits in the kernel's own snake order, with the
+    library's balanced table (trlm_attn_job_table; B8 T1024 is its 48-head,
+    16-block, 256-unit case) and with a random permutation of the jobs."""
+    HD = 64
+    D, N, nqb = H * HD, B * T, (T + 63) // 64
+    print("job placement case B%d H%d T%d" % (B, H, T), flush=True)
+    rng = np.random.default_rng(77 + T)
+    qkv = (0.5 * rng.standard_normal((N, 3 * D))).astype(np.float32)
+    tables = [None]
+    if B * H == 48 and nqb == 16:
+        t = (C.c_int32 * (B * H * nqb))()
+        assert trlm.libs()[1].trlm_attn_job_table(B * H, nqb, 256, t) == 1
+        tables.append(np.frombuffer(t, dtype=np.int32).copy())
+    perm = rng.permutation(B * H * nqb)
+    tables.append(((perm // (B * H)) << 16 | (perm % (B * H))).astype(np.int32))
+    dev = trlm.Device()
+    try:
+        f = dev.hip.hip_get_kernel(C.byref(dev.ctx), b"k_attn_fwd_hd64")
+        dq_ = dev.upload(qkv)
+        outs = []
+        for tab in tables:
+            dOut, dlse = dev.empty(N * D * 4), dev.empty(B * H * T * 4)
+            djobs = dev.upload(tab) if tab is not None else None
+            p = AttnParams(qkv=dq_, out=dOut, lse=dlse, B=B, T=T, H=H, D=D, ldq=3 * D, ldo=D,
+                           scale=float(1.0 / np.sqrt(HD)), jobs=djobs)
+            args = (C.c_void_p * 1)(C.cast(C.pointer(p), C.c_void_p))
+            dev.hip.hip_launch(f, B * H, nqb, 1, 256, 1, 1, 0, args)
+            outs.append((dev.download(dOut, (N, D)), dev.download(dlse, (B * H * T,))))
+    finally:
+        dev.close()
+    for O, lse in outs[1:]:
+        assert np.array_equal(O.view(np.uint32), outs[0][0].view(np.uint32))
+        assert np.array_equal(lse.view(np.uint32), outs[0][1].view(np.uint32))

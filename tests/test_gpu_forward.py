@@ -100,6 +100,28 @@ def test_forward_loss_keeps_logits(trlm, orc, V, D, H, L, F, T, B):
     assert np.array_equal(am, host_argmax(logits2))
 
 
+def test_attention_placement_table_keeps_bits(trlm, orc, monkeypatch):
+    """At B8 T1024 with 6 heads (48 x 16 forward attention jobs) the trainer
+    gives the attention forward its balanced placement table; the logits
+    equal, bit for bit, those of a trainer that keeps the kernel's own order
+    (TRLM_ATTN_SNAKE=1, read at creation)."""
+    V, D, H, L, F, T, B = 300, 384, 6, 1, 128, 1024, 8
+    model = orc.Model(V, D, H, L, F)
+    params = model.init(1337, 1)
+    ids = orc.random_tokens(B * T, V, 4242, 13, hi_exclusive=V)
+    got = []
+    for snake in ("0", "1"):
+        monkeypatch.setenv("TRLM_ATTN_SNAKE", snake)
+        hm = trlm.HostModel(V, D, H, L, F, params)
+        tr = trlm.Trainer(hm, B, T)
+        try:
+            got.append(tr.forward_logits(ids))
+        finally:
+            tr.destroy()
+            hm.close()
+    assert np.array_equal(got[0].view(np.uint32), got[1].view(np.uint32))
+
+
 GEMM_TILES = [None, "256x128", "128x256", "128x128", "128x128_k32", "64x128", "64x128_k32", "64x64", "64x64_k32"]
 
 

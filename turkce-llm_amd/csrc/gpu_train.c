@@ -142,6 +142,47 @@ static AttnParams attn_params(GpuTrainer* g) {
     return a;
 }
 
+/* The causal attention forward's job of each workgroup.  Query block q of a
+ * head is a job of q + 1 key-block stages, so a head's jobs have the sizes
+ * 1 .. n (n query blocks).  When the grid is exactly three resident
+ * workgroups per compute unit, workgroups L, L + cus and L + 2 cus share one
+ * unit (the dispatcher fills every unit once per round of `cus`
+ * workgroups), and the unit's time follows the sum of its three sizes.
+ * Three heads' jobs (three copies of 1 .. n) split into n triples whose sums
+ * are all floor or ceil of 3(n + 1)/2: row a is i = 1 .. n, row b is a
+ * shifted cyclically by n/2, and row c gives rank 1 .. n to the columns in
+ * descending order of a + b (ties: lower i first) -- each row a
+ * permutation of 1 .. n, so every (head, query block) is taken once.  Three
+ * heads per n units; B8 T1024 (48 heads, 16 blocks, 256 units): every unit
+ * gets 25 or 26 stages, against 23 to 28 in the kernel's snake order. */
+i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, i32* jobs) {
+    if (n == 0 || cus == 0 || heads % 3 != 0 || (u64)heads * n != 3ull * cus || n > 32767 || heads > 65535)
+        return 0;
+    u32* row = (u32*)malloc(3ull * n * sizeof(u32));
+    if (!row) fatal("out of host memory");
+    u32 *ra = row, *rb = row + n, *rc = row + 2 * n;
+    for (u32 i = 0; i < n; i++) {
+        ra[i] = i + 1;
+        rb[i] = (i + n / 2) % n + 1;
+    }
+    for (u32 i = 0; i < n; i++) {
+        u32 rank = 0;
+        for (u32 j = 0; j < n; j++) {
+            const u32 pi = ra[i] + rb[i], pj = ra[j] + rb[j];
+            rank += (pj > pi || (pj == pi && j < i)) ? 1u : 0u;
+        }
+        rc[i] = rank + 1;
+    }
+    for (u32 r = 0; r < heads / 3; r++)
+        for (u32 t = 0; t < n; t++)
+            for (u32 k = 0; k < 3; k++) {
+                const u32 size = row[k * n + t], head = 3 * r + k, unit = r * n + t;
+                jobs[k * cus + unit] = (i32)(((size - 1) << 16) | head);
+            }
+    free(row);
+    return 1;
+}
+
 /* ---------------- create / destroy ---------------- */
 
 /* Every device buffer of a trainer lives in one allocation, carved into
@@ -215,6 +256,7 @@ static void plan_buffers(GpuTrainer* g, CarvePlan* cp) {
     want_f(cp, &g->dh, N * F);
     want_f(cp, &g->dvec, BHT);
     want_f(cp, &g->att_ds, (u64)g->B * g->H * (nqb * (nqb + 1) / 2) * 4096);
+    want(cp, &g->attn_jobs, (u64)g->B * g->H * nqb * sizeof(i32));
     /* token ids and the embedding backward's row groups (u32) */
     want(cp, &g->ids, N * sizeof(u32));
     want(cp, &g->targets, N * sizeof(u32));
@@ -319,6 +361,23 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
     g.k.attn_bwd_dq = hip_get_kernel(c, name);
     snprintf(name, sizeof(name), "k_attn_dvec_hd%u", g.hd);
     g.k.attn_dvec = hip_get_kernel(c, name);
+    /* the attention forward's placement table, where the grid is exactly
+     * three resident workgroups per compute unit (TRLM_ATTN_SNAKE=1 keeps
+     * the kernel's own order; the results are the same bits either way) */
+    g.attn_fwd_jobs = 0;
+    {
+        const char* snake = getenv("TRLM_ATTN_SNAKE");
+        const u32 heads = g.B * g.H, nqb = (g.T + 63) / 64;
+        if (!(snake && snake[0] == '1') && hip_blocks_per_cu(g.k.attn_fwd, 256) == 3) {
+            i32* t = (i32*)malloc((u64)heads * nqb * sizeof(i32));
+            if (!t) fatal("out of host memory");
+            if (trlm_attn_job_table(heads, nqb, hip_cu_count(), t)) {
+                hip_h2d(g.attn_jobs, t, (u64)heads * nqb * sizeof(i32));
+                g.attn_fwd_jobs = g.attn_jobs;
+            }
+            free(t);
+        }
+    }
 
     gpu_trainer_upload(&g, params, NULL_PTR);
     hip_sync();
@@ -502,6 +561,7 @@ void trlm_forward_hidden(GpuTrainer* g, const u32* ids, TrlmLayerHook hook, void
         }
         if (hook) hook(hook_ctx, g, l, a->qkv);
         ap.qkv = (const float*)a->qkv; ap.out = (float*)a->att; ap.lse = (float*)a->lse;
+        ap.jobs = (const int*)g->attn_fwd_jobs;
         {
             void* args[] = { &ap };
             hip_launch(g->k.attn_fwd, g->B * g->H, cdiv_u64(g->T, 64), 1, 256, 1, 1, 0, args);

@@ -151,6 +151,20 @@ static HipCtx* current(const char* what) {
 
 hipStream_t hip_current_stream(void) { return current("hip_current_stream")->stream; }
 
+u32 hip_cu_count(void) {
+    int n = 0;
+    check(hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, current("hip_cu_count")->device),
+          "hipDeviceGetAttribute(multiprocessor count)");
+    return (u32)n;
+}
+
+u32 hip_blocks_per_cu(hipFunction_t f, u32 block_threads) {
+    int n = 0;
+    check(hipModuleOccupancyMaxActiveBlocksPerMultiprocessor(&n, f, (int)block_threads, 0),
+          "hipModuleOccupancyMaxActiveBlocksPerMultiprocessor");
+    return (u32)n;
+}
+
 hipFunction_t hip_get_kernel(HipCtx* c, const char* name) {
     hipFunction_t f;
     hipError_t r = hipModuleGetFunction(&f, c->module, name);

@@ -55,6 +55,10 @@ typedef struct AttnParams {
     // dK/dV pass's register order [key group g][query half c][r][lane]: key
     // 32g + l%32, query 32c + 8(r/4) + 4(l/32) + r%4 (one 256-byte row per r)
     float* ds;
+    // forward, optional: the job of workgroup L = blockIdx.y * gridDim.x +
+    // blockIdx.x as query block << 16 | (batch * H + head); without it the
+    // kernel takes its jobs in its own longest-first snake order
+    const int* jobs;
 } AttnParams;
 
 /* Fused decode GEMMs and head (kernels/decode_fused.hip, host gpu_decode.c) */

@@ -221,7 +221,10 @@ __device__ __forceinline__ void att_snake_job(int nqb, int& qb, int& bh) {
 // online softmax, and the two parts are merged at the end.  One K and one V^T
 // tile per stage (35 KB of LDS) and 167 registers let three workgroups share
 // a CU, so all 768 workgroups of B8 T1024 are resident at once and the
-// snake order (att_snake_job) evens out the causal work per CU.
+// snake order (att_snake_job) evens out the causal work per CU: 23 to 28 key
+// blocks.  When the grid is exactly three workgroups per CU, the host's job
+// table (p.jobs, trlm_attn_job_table) gives every CU 25 or 26 (B8 T1024:
+// 70.8 -> 66.7 us, same bits).
 template <int HD>
 __device__ void flash_fwd(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;
@@ -233,7 +236,16 @@ __device__ void flash_fwd(const AttnParams& p) {
     const int grp = wave & 1, part = wave >> 1;
     const int nqb = (p.T + 63) / 64;
     int qb, bh;
-    att_snake_job(nqb, qb, bh);
+    if (p.jobs) {
+        // the host's placement: workgroups L, L + CUs, L + 2 CUs share a
+        // compute unit, and their jobs' key-block counts sum to the same
+        // total (+-1) on every unit
+        const int j = p.jobs[blockIdx.y * gridDim.x + blockIdx.x];
+        qb = j >> 16;
+        bh = j & 0xffff;
+    } else {
+        att_snake_job(nqb, qb, bh);
+    }
     const int b = bh / p.H, h = bh - b * p.H;
     const long long rowbase = (long long)b * p.T;
     const float* qkv = p.qkv + rowbase * p.ldq;
