@@ -88,15 +88,16 @@ TrlmGemm* gpu_trainer_gemm_engine(GpuTrainer* g);
 
 /* Placement of the causal attention forward's jobs (host-only; no device
  * call).  For a grid of `heads` (batch x heads) by n query blocks that is
- * exactly three workgroups per compute unit (heads * n == 3 * cus, heads a
- * multiple of 3), fills jobs[heads * n] -- workgroup L = query-block index *
- * heads + head index takes query block jobs[L] >> 16 of head jobs[L] &
- * 0xffff -- so that the three workgroups L, L + cus, L + 2 cus that share a
- * compute unit hold floor or ceil of 3(n + 1)/2 key-block stages between
- * them, and returns 1; otherwise returns 0 and leaves jobs alone.  The
+ * exactly three workgroups per compute unit (heads * n == 3 * cus, heads / 3
+ * a multiple of xcds), fills jobs[heads * n] -- workgroup L = query-block
+ * index * heads + head index takes query block jobs[L] >> 16 of head
+ * jobs[L] & 0xffff -- so that the three workgroups L, L + cus, L + 2 cus
+ * that share a compute unit hold floor or ceil of 3(n + 1)/2 key-block
+ * stages between them and every head's jobs have the same L mod xcds (one
+ * XCD), and returns 1; otherwise returns 0 and leaves jobs alone.  The
  * trainer builds it when the forward kernel holds three workgroups per
  * compute unit; any table that is a permutation gives the same bits. */
-i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, i32* jobs);
+i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, u32 xcds, i32* jobs);
 
 /* ---- checkpoints: TRLM v1 (training/checkpoint.h:6-12), the reference's
  * format and rules (checkpoint.c:22-137), straight from / to the device.

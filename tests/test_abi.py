@@ -257,33 +257,40 @@ def test_gemm_plan_is_a_pure_function_of_the_shape(trlm):
 
 
 def test_attention_job_table(trlm):
-    """trlm_attn_job_table: every (query block, head) job exactly once, and the
+    """trlm_attn_job_table: every (query block, head) job exactly once; the
     three workgroups L, L + cus, L + 2 cus that share a compute unit hold
     floor or ceil of 3(n + 1)/2 key-block stages (query block q is q + 1
-    stages) -- checked by counting, for every n up to 64 and some larger, with
-    1, 2 and 16 triples of heads; B8 T1024 (48 heads, 16 blocks, 256 units)
-    gives 25 or 26 per unit.  Any grid that is not exactly three workgroups
-    per unit gets 0 and an untouched table."""
+    stages); and every head's workgroups have one L mod xcds (the XCD whose L2
+    holds that head's K and V) -- checked by counting, for every n up to 64
+    and some larger, with 1, 2 and 16 triples of heads per XCD over 1 to 8
+    XCDs; B8 T1024 (48 heads, 16 blocks, 256 units, 8 XCDs) gives 25 or 26
+    per unit.  Any grid that is not exactly three workgroups per unit, or
+    whose head triples do not divide among the XCDs, gets 0 and an untouched
+    table."""
     import numpy as np
     _, hip = trlm.libs()
     for n in list(range(1, 65)) + [100, 127, 128, 256]:
-        for trip in (1, 2, 16):
+        for trip, xcds in ((1, 1), (2, 2), (16, 8), (8, 8), (3, 1)):
             heads, cus = 3 * trip, trip * n
             jobs = (C.c_int32 * (heads * n))()
-            assert hip.trlm_attn_job_table(heads, n, cus, jobs) == 1
+            assert hip.trlm_attn_job_table(heads, n, cus, xcds, jobs) == 1
             a = np.frombuffer(jobs, dtype=np.int32)
             qb, hd = a >> 16, a & 0xFFFF
             assert sorted(zip(qb.tolist(), hd.tolist())) == [(q, h) for q in range(n) for h in range(heads)]
             stages = (qb + 1).reshape(3, cus).sum(axis=0)
             assert stages.min() >= 3 * (n + 1) // 2 and stages.max() <= -(-3 * (n + 1) // 2), (n, trip)
+            xcd = np.arange(heads * n) % xcds
+            for h in range(heads):
+                assert len(set(xcd[hd == h].tolist())) == 1, (n, trip, xcds, h)
     jobs = (C.c_int32 * 768)()
-    assert hip.trlm_attn_job_table(48, 16, 256, jobs) == 1
+    assert hip.trlm_attn_job_table(48, 16, 256, 8, jobs) == 1
     stages = ((np.frombuffer(jobs, dtype=np.int32) >> 16) + 1).reshape(3, 256).sum(axis=0)
     assert set(stages.tolist()) == {25, 26}
-    for heads, n, cus in [(48, 8, 256), (50, 16, 256), (48, 16, 255), (3, 16, 0), (48, 0, 256), (6, 4, 7)]:
+    for heads, n, cus, xcds in [(48, 8, 256, 8), (50, 16, 256, 8), (48, 16, 255, 8), (3, 16, 0, 1), (48, 0, 256, 8),
+                                (6, 4, 7, 1), (24, 16, 128, 16), (48, 16, 256, 0), (6, 4, 8, 4)]:
         size = max(1, heads * n)
         jobs = (C.c_int32 * size)(*([-7] * size))
-        assert hip.trlm_attn_job_table(heads, n, cus, jobs) == 0
+        assert hip.trlm_attn_job_table(heads, n, cus, xcds, jobs) == 0
         assert all(v == -7 for v in jobs)
 
 

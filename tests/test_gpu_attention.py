@@ -170,7 +170,7 @@ def test_forward_job_placement_keeps_bits(trlm, B, H, T):
     tables = [None]
     if B * H == 48 and nqb == 16:
         t = (C.c_int32 * (B * H * nqb))()
-        assert trlm.libs()[1].trlm_attn_job_table(B * H, nqb, 256, t) == 1
+        assert trlm.libs()[1].trlm_attn_job_table(B * H, nqb, 256, 8, t) == 1
         tables.append(np.frombuffer(t, dtype=np.int32).copy())
     perm = rng.permutation(B * H * nqb)
     tables.append(((perm // (B * H)) << 16 | (perm % (B * H))).astype(np.int32))

@@ -154,9 +154,13 @@ static AttnParams attn_params(GpuTrainer* g) {
  * descending order of a + b (ties: lower i first) -- each row a
  * permutation of 1 .. n, so every (head, query block) is taken once.  Three
  * heads per n units; B8 T1024 (48 heads, 16 blocks, 256 units): every unit
- * gets 25 or 26 stages, against 23 to 28 in the kernel's snake order. */
-i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, i32* jobs) {
-    if (n == 0 || cus == 0 || heads % 3 != 0 || (u64)heads * n != 3ull * cus || n > 32767 || heads > 65535)
+ * gets 25 or 26 stages, against 23 to 28 in the kernel's snake order.  Each
+ * triple of heads stays on one XCD, as the snake order keeps each head. */
+#define GFX950_XCDS 8u   /* MI355X: 8 XCDs of 32 compute units, each with its own L2 */
+
+i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, u32 xcds, i32* jobs) {
+    if (n == 0 || cus == 0 || xcds == 0 || heads % 3 != 0 || (u64)heads * n != 3ull * cus || n > 32767 ||
+        heads > 65535 || (heads / 3) % xcds != 0)
         return 0;
     u32* row = (u32*)malloc(3ull * n * sizeof(u32));
     if (!row) fatal("out of host memory");
@@ -173,10 +177,14 @@ i32 trlm_attn_job_table(u32 heads, u32 n, u32 cus, i32* jobs) {
         }
         rc[i] = rank + 1;
     }
+    /* replica r (heads 3r .. 3r + 2) takes units x, x + xcds, x + 2 xcds, ...
+     * of one XCD x = r mod xcds: workgroups go to the XCDs in turn (L mod
+     * xcds), so each head's K and V are read into one XCD's L2 only */
     for (u32 r = 0; r < heads / 3; r++)
         for (u32 t = 0; t < n; t++)
             for (u32 k = 0; k < 3; k++) {
-                const u32 size = row[k * n + t], head = 3 * r + k, unit = r * n + t;
+                const u32 size = row[k * n + t], head = 3 * r + k;
+                const u32 unit = r % xcds + xcds * ((r / xcds) * n + t);
                 jobs[k * cus + unit] = (i32)(((size - 1) << 16) | head);
             }
     free(row);
@@ -371,7 +379,7 @@ GpuTrainer gpu_trainer_create(Allocator* alloc, const char* ptx_path, const LMMo
         if (!(snake && snake[0] == '1') && hip_blocks_per_cu(g.k.attn_fwd, 256) == 3) {
             i32* t = (i32*)malloc((u64)heads * nqb * sizeof(i32));
             if (!t) fatal("out of host memory");
-            if (trlm_attn_job_table(heads, nqb, hip_cu_count(), t)) {
+            if (trlm_attn_job_table(heads, nqb, hip_cu_count(), GFX950_XCDS, t)) {
                 hip_h2d(g.attn_jobs, t, (u64)heads * nqb * sizeof(i32));
                 g.attn_fwd_jobs = g.attn_jobs;
             }

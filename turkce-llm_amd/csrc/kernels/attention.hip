@@ -223,9 +223,9 @@ __device__ __forceinline__ void att_snake_job(int nqb, int& qb, int& bh) {
 // a CU, so all 768 workgroups of B8 T1024 are resident at once and the
 // snake order (att_snake_job) evens out the causal work per CU: 23 to 28 key
 // blocks.  When the grid is exactly three workgroups per CU, the host's job
-// table (p.jobs, trlm_attn_job_table) gives every CU 25 or 26 (B8 T1024,
-// same bits: 70.8 -> 66.7 us launched back to back, ~2.8 us less after the
-// QKV projection GEMM, ~1 us per layer in the model's forward).
+// table (p.jobs, trlm_attn_job_table) gives every CU 25 or 26 and keeps each
+// head on one XCD as the snake does (B8 T1024, same bits: 70.8 -> 66.7 us
+// launched back to back; within noise in the model's forward).
 template <int HD>
 __device__ void flash_fwd(const AttnParams& p) {
     constexpr int DB = (HD + 31) / 32;

@@ -223,7 +223,8 @@ def _bind(host, hip):
     _sig(hip, "trlm_gemm_plan", C.c_char_p, [C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_int32, C.c_uint32,
                                              C.POINTER(C.c_int32)])
     _sig(hip, "trlm_gemm_force", C.c_int32, [C.c_void_p, C.c_char_p, C.c_int32])
-    _sig(hip, "trlm_attn_job_table", C.c_int32, [C.c_uint32, C.c_uint32, C.c_uint32, C.POINTER(C.c_int32)])
+    _sig(hip, "trlm_attn_job_table", C.c_int32, [C.c_uint32, C.c_uint32, C.c_uint32, C.c_uint32,
+                                                 C.POINTER(C.c_int32)])
     TP = C.POINTER(TrlmTimer)
     _sig(hip, "trlm_timer_create", None, [TP])
     _sig(hip, "trlm_timer_destroy", None, [TP])
